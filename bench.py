@@ -1,0 +1,426 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized MoE gather_qmm path on one MI355X.
+
+Headline (``value``): the decode gate_up gather_qmm with fused SwiGLU --
+1 token, hidden 2048, 256 experts, top-10, fused gate_up W [256, 1024, 2048]
+4-bit group 64 -- in HBM GB/s of algorithmic bytes (each routed expert's packed
+codes + scales + biases once, plus x in and h out).  One step is one call.
+
+Method: every step reads a different weight set and a different set of 10
+experts (weight sets rotated over >= 1.2 GB so the 256 MB Infinity Cache cannot
+serve them), the K timed launches are captured in one HIP graph, and the graph
+is timed with events on the stream it is replayed on.  The other four
+workloads are measured the same way and reported under ``configs``; the CPU
+baseline is the oracle's C restatement timed on this host.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--configs 0,1,2,3,4]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, vendor spec
+BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA, vendor spec
+INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, vendor spec
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--configs", default="0,1,2,3,4")
+    ap.add_argument("--rotate-gb", type=float, default=1.2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default=None, help="run one workload's timed loop only (for profiling)")
+    return ap.parse_args()
+
+
+def to_dev(a, dtype, dev):
+    import torch
+
+    a = np.ascontiguousarray(a)
+    if dtype == "bf16":
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)
+    if dtype == "words":
+        return torch.from_numpy(a.view(np.int32)).to(dev)
+    return torch.from_numpy(a).to(dev)
+
+
+def random_like_words(shape, dev, gen):
+    import torch
+
+    return torch.randint(-2 ** 31, 2 ** 31 - 1, shape, dtype=torch.int32, device=dev, generator=gen)
+
+
+def random_scales(shape, dev, gen):
+    import torch
+
+    s = torch.rand(shape, device=dev, generator=gen) * 0.015 + 0.005
+    return s.to(torch.bfloat16)
+
+
+def random_biases(shape, dev, gen):
+    import torch
+
+    return (torch.randn(shape, device=dev, generator=gen) * 0.05).to(torch.bfloat16)
+
+
+def weight_sets(wl, n_sets, dev, seed):
+    """Set 0 is the seeded workload; the others are fresh random sets on the device."""
+    import torch
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    sets = [(to_dev(wl["w"], "words", dev), to_dev(wl["s"], "bf16", dev), to_dev(wl["b"], "bf16", dev))]
+    for _ in range(1, n_sets):
+        sets.append((random_like_words(wl["w"].shape, dev, gen), random_scales(wl["s"].shape, dev, gen),
+                     random_biases(wl["b"].shape, dev, gen)))
+    return sets
+
+
+def n_sets_for(wl, rotate_gb):
+    per = wl["w"].nbytes + wl["s"].nbytes + wl["b"].nbytes
+    return max(1, int(np.ceil(rotate_gb * 1e9 / per)))
+
+
+def time_graph(fn_list, warmup, dev):
+    """Capture the launches in fn_list (one per step) into a graph, replay once
+    untimed after `warmup` eager steps, then time one replay with events on
+    the replay stream.  Returns seconds per step."""
+    import torch
+
+    for i in range(warmup):
+        fn_list[i % len(fn_list)]()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for fn in fn_list:
+                fn()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / len(fn_list), g
+
+
+# --------------------------------------------------------------- workloads
+
+
+def setup_cfg1(args, dev):
+    """Decode gate_up + SwiGLU: 10 experts of one token."""
+    import torch
+    from titan_amd import ops, synth
+
+    wl = synth.make(1)
+    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 101)
+    rng = np.random.default_rng(1001)
+    x = to_dev(wl["x"], "bf16", dev)
+    E = wl.meta["E"]
+    perms = [rng.permutation(E) for _ in sets]
+    cursor = [0] * len(sets)
+    idxs = []
+    for i in range(args.steps):
+        si = i % len(sets)
+        if cursor[si] + 10 > E:
+            perms[si] = rng.permutation(E)
+            cursor[si] = 0
+        idxs.append(torch.from_numpy(perms[si][cursor[si]:cursor[si] + 10].astype(np.int32)[None]).to(dev))
+        cursor[si] += 10
+    idxs[0] = to_dev(wl["idx"], "i32", dev)
+    outs = [torch.empty(1, 10, 512, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+
+    def mk(i):
+        w, s, b = sets[i % len(sets)]
+        idx = idxs[i]
+
+        def f():
+            ops._lib.call("qmoe_moe_gate_up_swiglu", x.data_ptr(), idx.data_ptr(), 1, 10, 2048, w.data_ptr(),
+                          s.data_ptr(), b.data_ptr(), 256, 512, 64, 4, outs[i % 2].data_ptr(),
+                          torch.cuda.current_stream().cuda_stream)
+        return f
+
+    return wl, [mk(i) for i in range(args.steps)], {
+        "bytes": synth.algorithmic_bytes(1), "flops": synth.algorithmic_flops(1), "bound": "hbm",
+        "kernel": "qmv_kernel<4,16,1>", "sets": len(sets),
+        "workload": "decode gate_up gather_qmm + SwiGLU: 1 token, H=2048, E=256, top_k=10, "
+                    "W [256,1024,2048] int4 g64 bf16 scale/bias -> h [10,512]"}
+
+
+def setup_cfg0(args, dev):
+    import torch
+    from titan_amd import ops, synth
+
+    wl = synth.make(0)
+    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 100)
+    x = to_dev(wl["x"], "bf16", dev)
+    out = torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)
+
+    def mk(i):
+        w, s, b = sets[i % len(sets)]
+
+        def f():
+            ops._lib.call("qmoe_quantized_matmul", x.data_ptr(), 1, 2048, w.data_ptr(), s.data_ptr(),
+                          b.data_ptr(), 4096, 64, 4, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        return f
+
+    return wl, [mk(i) for i in range(args.steps)], {
+        "bytes": synth.algorithmic_bytes(0), "flops": synth.algorithmic_flops(0), "bound": "hbm",
+        "kernel": "qmv_kernel<4,16,0>", "sets": len(sets),
+        "workload": "dense quantized_matmul x [1,2048] . W [4096,2048] int4 g64"}
+
+
+def setup_cfg2(args, dev):
+    import torch
+    from titan_amd import ops, synth
+
+    wl = synth.make(2)
+    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 102)
+    h = to_dev(wl["h"], "bf16", dev)
+    idx = to_dev(wl["idx"], "i32", dev)
+    sc = to_dev(wl["scores"], "f32", dev)
+    rng = np.random.default_rng(1002)
+    # per step: a fresh routing (same distinct-expert statistics), cycled over sets
+    idxs = [idx]
+    for i in range(1, args.steps):
+        idxs.append(torch.from_numpy(np.stack([rng.choice(256, 10, replace=False) for _ in range(8)])
+                                     .astype(np.int32)).to(dev))
+    distinct = [int(torch.unique(t).numel()) for t in idxs]
+    y = torch.empty(8, 2048, dtype=torch.bfloat16, device=dev)
+
+    def mk(i):
+        w, s, b = sets[i % len(sets)]
+        ii = idxs[i]
+
+        def f():
+            ops._lib.call("qmoe_moe_down_wsum", h.data_ptr(), ii.data_ptr(), sc.data_ptr(), 8, 10, 512,
+                          w.data_ptr(), s.data_ptr(), b.data_ptr(), 256, 2048, 64, 4, y.data_ptr(),
+                          torch.cuda.current_stream().cuda_stream)
+        return f
+
+    mean_distinct = float(np.mean(distinct))
+    row_bytes = 512 // 2 + 8 * 4
+    bytes_ = int(mean_distinct * 2048 * row_bytes + 8 * 10 * 512 * 2 + 8 * 2048 * 2 + 8 * 10 * 4)
+    return wl, [mk(i) for i in range(args.steps)], {
+        "bytes": bytes_, "flops": synth.algorithmic_flops(2, wl), "bound": "hbm",
+        "kernel": "down_wsum_kernel<1,16>", "sets": len(sets), "mean_distinct_experts": mean_distinct,
+        "workload": "decode down + top-10 weighted sum: 8 tokens, I=512, D=2048, E=256, "
+                    "W [256,2048,512] int4 g64 -> y [8,2048]"}
+
+
+def _prefill_common(args, dev, cfg):
+    import torch
+    from titan_amd import ops, synth
+
+    wl = synth.make(cfg)
+    T, k = wl["idx"].shape
+    x = to_dev(wl["x"], "bf16", dev)
+    sets = weight_sets(wl, 2, dev, 100 + cfg)
+    r = ops.route(to_dev(wl["idx"], "i32", dev), 256)
+    lhs = torch.div(r.order, k, rounding_mode="floor").to(torch.int32)
+    out = torch.empty(T * k, 1024, dtype=torch.bfloat16, device=dev)
+    return wl, x, sets, r, lhs, out
+
+
+def setup_cfg3(args, dev):
+    import torch
+    from titan_amd import ops, synth
+
+    wl, x, sets, r, lhs, out = _prefill_common(args, dev, 3)
+    t = r.tiles
+    steps = max(1, args.steps // 10)
+
+    def mk(i):
+        w, s, b = sets[i % len(sets)]
+
+        def f():
+            ops._lib.call("qmoe_gather_qmm_sorted", x.data_ptr(), lhs.data_ptr(), t.rows, 2048, w.data_ptr(),
+                          s.data_ptr(), b.data_ptr(), 256, 1024, 64, 4, t.offsets.data_ptr(),
+                          t.tile_row.data_ptr(), t.tile_exp.data_ptr(), t.ntiles.data_ptr(), t.maxt,
+                          out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        return f
+
+    return wl, [mk(i) for i in range(steps)], {
+        "flops": synth.algorithmic_flops(3, wl), "bound": "mfma", "peak_tflops": BF16_PEAK_TFLOPS,
+        "kernel": "gemm_bf16_kernel", "sets": len(sets),
+        "workload": "prefill grouped GEMM: 4096 tokens x top-10 Zipf(1.1) routed rows sorted by expert, "
+                    "gate_up W [256,1024,2048] int4 g64, x gathered in-kernel -> [40960,1024]"}
+
+
+def setup_cfg4(args, dev):
+    import torch
+    from titan_amd import ops, synth
+
+    wl, x, sets, r, lhs, out = _prefill_common(args, dev, 4)
+    t = r.tiles
+    T = wl.meta["T"]
+    xi = torch.empty(T, 2048, dtype=torch.int8, device=dev)
+    sx = torch.empty(T, dtype=torch.float32, device=dev)
+    steps = max(1, args.steps // 10)
+
+    def mk(i):
+        w, s, b = sets[i % len(sets)]
+
+        def f():
+            st = torch.cuda.current_stream().cuda_stream
+            ops._lib.call("qmoe_quantize_act_int8", x.data_ptr(), T, 2048, xi.data_ptr(), sx.data_ptr(), st)
+            ops._lib.call("qmoe_gather_qmm_int8_sorted", xi.data_ptr(), sx.data_ptr(), lhs.data_ptr(), t.rows,
+                          2048, w.data_ptr(), s.data_ptr(), b.data_ptr(), 256, 1024, 64, 4,
+                          t.offsets.data_ptr(), t.tile_row.data_ptr(), t.tile_exp.data_ptr(),
+                          t.ntiles.data_ptr(), t.maxt, out.data_ptr(), st)
+        return f
+
+    return wl, [mk(i) for i in range(steps)], {
+        "flops": synth.algorithmic_flops(4, wl), "bound": "mfma", "peak_tflops": INT8_PEAK_TOPS,
+        "kernel": "quant_act_kernel + gemm_int8_kernel", "sets": len(sets),
+        "workload": "int8-activation x int4-weight gate_up prefill: 4096 tokens x top-10 Zipf(1.1), "
+                    "per-token symmetric int8 x, W [256,1024,2048] int4 g64 -> [40960,1024]"}
+
+
+SETUPS = {0: setup_cfg0, 1: setup_cfg1, 2: setup_cfg2, 3: setup_cfg3, 4: setup_cfg4}
+
+
+# ------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline(cfg, wl, budget_s):
+    """The oracle (C, OpenMP) on the same seeded inputs, timed on this host."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from titan_amd import synth
+
+    oracle.build()
+    threads = oracle.max_threads()
+    if cfg == 1:
+        def run():
+            gu, _ = oracle.gather_qmm_rows(wl["x"], np.zeros(10, np.int32), wl["idx"].reshape(-1), wl["w"],
+                                           wl["s"], wl["b"])
+            oracle.swiglu(gu)
+        work, unit = synth.algorithmic_bytes(1), "GB/s"
+        sample = "full workload: 10 experts x 1024 rows x 2048, fp64 accumulation"
+    elif cfg == 0:
+        def run():
+            oracle.gather_qmm_rows(wl["x"], None, np.zeros(1, np.int32), wl["w"][None], wl["s"][None],
+                                   wl["b"][None])
+        work, unit = synth.algorithmic_bytes(0), "GB/s"
+        sample = "full workload"
+    else:
+        return None
+    run()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= 1000:
+            break
+    per = el / reps
+    return {"value": round(work / per / 1e9, 3), "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{sample}; {reps} repetitions in {el:.1f} s; {per * 1e3:.2f} ms per call",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------------- main
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the expert-parallel "
+                                   "sharding is design-only, see DESIGN.md)"}))
+        return 2
+    import torch
+    from titan_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    cfgs = [int(c) for c in args.configs.split(",") if c != ""]
+    if args.only is not None:
+        cfgs = [int(args.only)]
+    results = {}
+    head = None
+    for cfg in cfgs:
+        print(f"[bench] workload {cfg}: setup", file=sys.stderr, flush=True)
+        wl, fns, meta = SETUPS[cfg](args, dev)
+        print(f"[bench] workload {cfg}: timing {len(fns)} steps", file=sys.stderr, flush=True)
+        sec, _g = time_graph(fns, args.warmup, dev)
+        res = {"workload": meta["workload"], "us_per_call": round(sec * 1e6, 3), "kernel": meta["kernel"],
+               "weight_sets": meta["sets"]}
+        if meta["bound"] == "hbm":
+            gbs = meta["bytes"] / sec / 1e9
+            res.update(metric="HBM GB/s", value=round(gbs, 1), bytes_per_call=meta["bytes"],
+                       pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2))
+        else:
+            tf = meta["flops"] / sec / 1e12
+            res.update(metric="TFLOP/s" if cfg == 3 else "TOP/s", value=round(tf, 1),
+                       flops_per_call=meta["flops"], pct_peak=round(100 * tf / meta["peak_tflops"], 2),
+                       pct_bf16_peak=round(100 * tf / BF16_PEAK_TFLOPS, 2))
+        for k_ in ("mean_distinct_experts",):
+            if k_ in meta:
+                res[k_] = meta[k_]
+        results[cfg] = res
+        print(f"[bench] workload {cfg}: {res}", file=sys.stderr, flush=True)
+        if cfg == 1:
+            head = (wl, meta, sec)
+        del fns, _g
+        torch.cuda.empty_cache()
+    if args.only is not None:
+        return 0
+    if head is None:
+        print(json.dumps({"configs": results}))
+        return 0
+    wl, meta, sec = head
+    gbs = meta["bytes"] / sec / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(1, wl, args.cpu_seconds)
+    line = {
+        "metric": "MoE gather_qmm HBM GB/s (decode gate_up, 1 token, top-10)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int4 weights (bf16 scale/bias), bf16 activations, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": meta["workload"], "tokens": 1, "top_k": 10, "experts": 256, "hidden": 2048,
+                   "intermediate": 512, "group_size": 64, "bits": 4, "weight_sets_rotated": meta["sets"]},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "configs": results,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

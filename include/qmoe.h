@@ -1,0 +1,204 @@
+/*
+ * qmoe.h -- C ABI of libqmoe.so, the MI355X (gfx950) quantized mixture-of-experts
+ * matmul path: MLX-affine group-quantized weights, gather_qmm for the fused
+ * gate_up and down expert projections, the int8-activation x int4-weight
+ * gate_up variant, and the fused SwiGLU / top-k weighted-sum epilogues.
+ *
+ * Conventions (every entry point):
+ *  - Plain device pointers and sizes; no framework types.  bf16 tensors are
+ *    uint16_t bit patterns; packed weights are uint32_t words in MLX affine
+ *    layout: element k of a row sits in word k*bits/32 at bit offset
+ *    bits*(k mod 32/bits), low bits first.  Scales and biases are bf16
+ *    [rows, K/group_size]; the weight is w = scale*q + bias.
+ *  - All tensors are contiguous, row-major.  Expert tensors are
+ *    [num_experts, N, K*bits/32] (weights) and [num_experts, N, K/group_size]
+ *    (scales, biases).
+ *  - The caller owns and allocates every output and workspace.  The library
+ *    never allocates or frees caller memory and keeps no state between calls
+ *    beyond a thread-local error message.
+ *  - Every launch is enqueued on `stream` (a hipStream_t; NULL is the null
+ *    stream).  No entry point synchronises the host.
+ *  - Return value: QMOE_OK, or an error code with a message readable through
+ *    qmoe_last_error().  QMOE_ERR_UNSUPPORTED means "this shape, dtype, bit
+ *    width or group size has no kernel": callers fall back to their stock
+ *    path, as the reference's patches do (engine/patches/moe-int8/patch.py:78-122).
+ *
+ * Each declaration names the reference interface it replaces (paths relative
+ * to the reference repository root).
+ */
+#ifndef QMOE_H
+#define QMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QMOE_ABI_VERSION 1
+
+enum {
+  QMOE_OK = 0,
+  QMOE_ERR_INVALID = 1,     /* bad argument (null pointer, inconsistent sizes) */
+  QMOE_ERR_UNSUPPORTED = 2, /* no kernel for this configuration: fall back */
+  QMOE_ERR_HIP = 3,         /* a HIP runtime call failed */
+  QMOE_ERR_WORKSPACE = 4    /* workspace missing or too small */
+};
+
+/* Weighted-sum rounding modes: titan/kernels/moe_weighted_sum.py:44-49. */
+enum { QMOE_WSUM_FAST = 0, QMOE_WSUM_OPS = 1, QMOE_WSUM_CLONE = 2 };
+
+int qmoe_abi_version(void);
+/* Thread-local message of the last failing call on this thread. */
+const char* qmoe_last_error(void);
+
+/* ---------------------------------------------------------------- layout --
+ * MLX affine unpack (layout contract evidenced by
+ * tests/kernels/test_moe_gather_int8.py:104-115) and materialised dequant
+ * out = bf16_rne(fmaf(q, s, b)) (titan/kernels/moe_gather_ws.py:343-344),
+ * the device counterparts of mx.dequantize. */
+int qmoe_unpack(const uint32_t* w, int64_t n_words, int bits, uint8_t* codes,
+                void* stream);
+int qmoe_dequantize(const uint32_t* w, const uint16_t* scales,
+                    const uint16_t* biases, int64_t rows, int64_t K,
+                    int group_size, int bits, uint16_t* out, void* stream);
+
+/* --------------------------------------------------------------- routing --
+ * Replaces _gather_sort (titan/adapters/mlx/vendor/mlx_lm/models/
+ * switch_layers.py:13-18) together with build_tiles
+ * (titan/kernels/moe_gather_ws.py:181-202), on the device, no host sync:
+ *   order      [n] pair index of sorted row i (stable argsort of ids)
+ *   inv_order  [n] argsort(order)
+ *   sorted_ids [n] ids[order]
+ *   offsets    [E+1] first sorted row of each expert (lower_bound)
+ *   tile_row / tile_exp [max_tiles] one (row_start, expert) per tile_rows
+ *              rows of each expert, expert-major; entries past the count are 0
+ *   ntiles     [1] number of tiles, capped at max_tiles
+ * max_tiles >= ceil(n/tile_rows) + E always suffices (moe_gather_ws.py:176-178).
+ * Ids outside [0, E) are clamped into range and counted in workspace word 0
+ * (readable after the stream completes), so every index written stays valid.
+ * Workspace: qmoe_route_workspace_size(n, E) bytes. */
+size_t qmoe_route_workspace_size(int64_t n_pairs, int32_t num_experts);
+int qmoe_route(const int32_t* ids, int64_t n_pairs, int32_t num_experts,
+               int32_t tile_rows, int32_t* order, int32_t* inv_order,
+               int32_t* sorted_ids, int32_t* offsets, int32_t* tile_row,
+               int32_t* tile_exp, int32_t* ntiles, int64_t max_tiles,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* build_tiles over ids that are already sorted ascending
+ * (titan/kernels/moe_gather_ws.py:133-156,181-202). */
+int qmoe_build_tiles(const int32_t* sorted_ids, int64_t n_rows,
+                     int32_t num_experts, int32_t tile_rows, int32_t* offsets,
+                     int32_t* tile_row, int32_t* tile_exp, int32_t* ntiles,
+                     int64_t max_tiles, void* stream);
+
+/* ------------------------------------------------------------ gather_qmm --
+ * Row form of mx.gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices,
+ * transpose=True, group_size, bits) (called at switch_layers.py:87-98;
+ * positional contract engine/patches/moe-int8/patch.py:81-90):
+ *   out[r, n] = sum_k x[x_rows[r], k] * W[experts[r]][n, k]
+ * x_rows == NULL means x_rows[r] = r (x already gathered).  A caller maps the
+ * broadcast (lhs_indices, rhs_indices) batch onto rows; rows need not be sorted.
+ * Matrix-vector kernel: every row streams its expert's weights, so this is the
+ * decode / small-batch path.  fp32 accumulation of the factored affine form
+ * s*sum(x*q) + b*sum(x) (engine/patches/decode-fusion/fused_kernels.py:57-79),
+ * bf16 output. */
+int qmoe_gather_qmv(const uint16_t* x, const int32_t* x_rows,
+                    const int32_t* experts, int64_t n_rows, int64_t K,
+                    const uint32_t* w, const uint16_t* scales,
+                    const uint16_t* biases, int32_t num_experts, int64_t N,
+                    int group_size, int bits, uint16_t* out, void* stream);
+
+/* mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)
+ * for x [M, K] (titan/adapters/mlx/compiled.py:209-218; small-M drop-in
+ * engine/patches/smallm/kernel.py:333-391): out [M, N]. */
+int qmoe_quantized_matmul(const uint16_t* x, int64_t M, int64_t K,
+                          const uint32_t* w, const uint16_t* scales,
+                          const uint16_t* biases, int64_t N, int group_size,
+                          int bits, uint16_t* out, void* stream);
+
+/* Sorted grouped GEMM: the prefill form of gather_qmm with
+ * sorted_indices=True, replacing titan/kernels/moe_gather_ws.py:417-445
+ * (and its MLX reference :403-414).  Rows [0, n_rows) are grouped by expert
+ * as described by (offsets, tile_row, tile_exp, ntiles) from qmoe_route or
+ * qmoe_build_tiles built with tile_rows == qmoe_gemm_tile_rows().
+ *   out[r, n] = sum_k x[x_rows[r], k] * W[e(r)][n, k]   (x_rows NULL: identity)
+ * Weights are dequantised to bf16 as bf16_rne(fmaf(q, s, b)) and multiplied on
+ * bf16 MFMA with fp32 accumulation (moe_gather_ws.py:20-32 semantics). */
+int qmoe_gemm_tile_rows(void);
+int qmoe_gather_qmm_sorted(const uint16_t* x, const int32_t* x_rows,
+                           int64_t n_rows, int64_t K, const uint32_t* w,
+                           const uint16_t* scales, const uint16_t* biases,
+                           int32_t num_experts, int64_t N, int group_size,
+                           int bits, const int32_t* offsets,
+                           const int32_t* tile_row, const int32_t* tile_exp,
+                           const int32_t* ntiles, int64_t max_tiles,
+                           uint16_t* out, void* stream);
+
+/* ------------------------------------------------------ fused decode MoE --
+ * Gather gate_up GEMV + SwiGLU in one launch, replacing
+ * engine/patches/decode-fusion/fused_kernels.py:31-88,194-210 (gate_up_silu)
+ * and the split + swiglu of switch_layers.py:229-237:
+ *   g = x[t] . W[idx[t,j]][i, :],  u = x[t] . W[idx[t,j]][I + i, :]
+ *   h[t, j, i] = bf16(silu(g) * u)         (fp32 throughout, gate rows first)
+ * x [T, K] bf16, idx [T, top_k] int32, w [E, 2I, K*bits/32]. */
+int qmoe_moe_gate_up_swiglu(const uint16_t* x, const int32_t* idx, int64_t T,
+                            int64_t top_k, int64_t K, const uint32_t* w,
+                            const uint16_t* scales, const uint16_t* biases,
+                            int32_t num_experts, int64_t I, int group_size,
+                            int bits, uint16_t* h, void* stream);
+
+/* Gather down GEMV + router-weighted top-k sum in one launch, replacing
+ * engine/patches/decode-fusion/fused_kernels.py:93-169,213-231 (down_wsum)
+ * and the weighted-sum tail of qwen3_5_moe/language.py:78-83:
+ *   y[t, :] = bf16( sum_j scores[t, j] * (W[idx[t,j]] @ h[t, j, :]) )
+ * Each distinct expert's weights are read once and shared by every (t, j)
+ * routed to it.  h [T, top_k, I] bf16, scores [T, top_k] fp32,
+ * w [E, D, I*bits/32], y [T, D] bf16.  T*top_k <= 1024. */
+int qmoe_moe_down_wsum(const uint16_t* h, const int32_t* idx,
+                       const float* scores, int64_t T, int64_t top_k,
+                       int64_t I, const uint32_t* w, const uint16_t* scales,
+                       const uint16_t* biases, int32_t num_experts, int64_t D,
+                       int group_size, int bits, uint16_t* y, void* stream);
+
+/* ----------------------------------------------------------- weighted sum --
+ * moe_weighted_sum (titan/kernels/moe_weighted_sum.py:142-195):
+ *   out[r, d] = sum_j sc[r, j] * xs[src, d],  src = inv_order[r*k + j]
+ * (inv_order NULL: src = r*k + j, the token-major layout).  mode is one of
+ * QMOE_WSUM_*: fast keeps fp32 scores and products; ops rounds scores and
+ * products to bf16; clone also keeps the eight partial sums in bf16.  Eight
+ * partial slots (j mod 8) combined in order; no fused multiply-add.
+ * xs [rows*k, dim] bf16, scores [rows, k] fp32, out [rows, dim] bf16. */
+int qmoe_weighted_sum(const uint16_t* xs, const int32_t* inv_order,
+                      const float* scores, int64_t rows, int64_t top_k,
+                      int64_t dim, int mode, uint16_t* out, void* stream);
+
+/* ------------------------------------------------------------------ int8 --
+ * int8-activation x int4-weight gate_up (replaces
+ * titan/kernels/moe_gather_int8.py:132-182 quantize_activations and
+ * :393-425 metal, with per-token symmetric activations):
+ *   sx[r] = max_k |x[r,k]| / 127 (fp32),  xi = clamp(rint(x / sx), -127, 127)
+ * A row of zeros gives sx = 0 and xi = 0. */
+int qmoe_quantize_act_int8(const uint16_t* x, int64_t R, int64_t K,
+                           int8_t* xi, float* sx, void* stream);
+
+/* out[r, n] = sx[x_rows[r]] * sum_g ( s[n,g] * D_g + b[n,g] * R_g ),
+ * D_g = sum_{k in g} xi*q and R_g = sum_{k in g} xi exact in int32, on int8
+ * MFMA; rows grouped by expert as for qmoe_gather_qmm_sorted with tile_rows
+ * == qmoe_gemm_tile_rows(). */
+int qmoe_gather_qmm_int8_sorted(const int8_t* xi, const float* sx,
+                                const int32_t* x_rows, int64_t n_rows,
+                                int64_t K, const uint32_t* w,
+                                const uint16_t* scales, const uint16_t* biases,
+                                int32_t num_experts, int64_t N, int group_size,
+                                int bits, const int32_t* offsets,
+                                const int32_t* tile_row,
+                                const int32_t* tile_exp, const int32_t* ntiles,
+                                int64_t max_tiles, uint16_t* out,
+                                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMOE_H */

@@ -1,0 +1,335 @@
+"""HIP path against the CPU oracle on the same seeded inputs.
+
+Bars: unpack, dequant, routing indices and the weighted-sum modes are
+bit-exact; matmul outputs are within 1 bf16 ULP of the RNE-rounded fp64 golden
+on live elements (|ref| >= max|ref|/256, the rule of
+engine/patches/round2/wsum10/test_exact.py:61-62) and within 2^-8 of max|ref|
+in max-abs error everywhere (engine/patches/decode-fusion/test_exact.py:53-57).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close_bf16, bf16_t, bits, f32_t, i32_t, words_t
+from titan_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+# ------------------------------------------------------------------ layout
+
+
+@pytest.mark.parametrize("bits_", [4, 8])
+def test_unpack_bit_exact(dev, orc, bits_):
+    say(f"unpack bits={bits_}")
+    rng = np.random.default_rng(11)
+    w = rng.integers(0, 2 ** 32, size=(64, 96), dtype=np.uint32)
+    got = ops.unpack(words_t(w, dev), bits_).cpu().numpy()
+    assert np.array_equal(got, orc.unpack(w, bits_))
+
+
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (4, 32), (8, 64), (4, 128)])
+def test_dequantize_bit_exact(dev, orc, bits_, gs):
+    say(f"dequantize bits={bits_} gs={gs}")
+    rng = np.random.default_rng(12)
+    K = 512
+    w, s, b = synth.quant_weights(rng, (3, 40), K, gs, bits_)
+    got = bits(ops.dequantize(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), gs, bits_))
+    assert np.array_equal(got, orc.dequantize_bf16(w, s, b, gs, bits_))
+
+
+# ----------------------------------------------------------------- routing
+
+
+def _route_cases():
+    rng = np.random.default_rng(5)
+    wl = synth.make(3, tokens=4096)
+    yield "cfg3-zipf", wl["idx"], 256
+    yield "one-expert", np.zeros(300, np.int32), 8
+    yield "uniform", rng.integers(0, 32, size=200).astype(np.int32), 32
+    yield "single", np.array([3], np.int32), 8
+    yield "ragged", rng.integers(0, 1000, size=12345).astype(np.int32), 1000
+
+
+@pytest.mark.parametrize("case", list(range(5)))
+def test_route_matches_stable_sort(dev, orc, case):
+    name, ids, E = list(_route_cases())[case]
+    say(f"route {name} n={ids.size} E={E}")
+    r = ops.route(i32_t(ids, dev), E)
+    order, inv, srt = orc.route_sort(ids, E)
+    assert np.array_equal(r.order.cpu().numpy(), order)
+    assert np.array_equal(r.inv_order.cpu().numpy(), inv)
+    assert np.array_equal(r.sorted_ids.cpu().numpy(), srt)
+    assert np.array_equal(order, np.argsort(ids.reshape(-1), kind="stable"))
+    off, trow, texp, nt = orc.build_tiles(srt, E, r.tiles.tile_rows)
+    assert np.array_equal(r.tiles.offsets.cpu().numpy(), off)
+    assert int(r.tiles.ntiles.item()) == nt
+    assert np.array_equal(r.tiles.tile_row.cpu().numpy(), trow)
+    assert np.array_equal(r.tiles.tile_exp.cpu().numpy(), texp)
+    assert int(r.bad_ids.item()) == 0
+
+
+def test_route_clamps_out_of_range_ids(dev, orc):
+    say("route out-of-range ids")
+    ids = np.array([0, 5, 9, -1, 3, 12, 5], np.int32)
+    r = ops.route(i32_t(ids, dev), 8)
+    assert int(r.bad_ids.item()) == 3
+    clamped = np.clip(ids, 0, 7)
+    order, inv, srt = orc.route_sort(clamped, 8)
+    assert np.array_equal(r.order.cpu().numpy(), order)
+    assert np.array_equal(r.sorted_ids.cpu().numpy(), srt)
+
+
+def test_build_tiles_from_sorted(dev, orc):
+    say("build_tiles sorted")
+    rng = np.random.default_rng(9)
+    ids = np.sort(rng.integers(0, 64, size=5000)).astype(np.int32)
+    t = ops.build_tiles(i32_t(ids, dev), 64, 48)
+    off, trow, texp, nt = orc.build_tiles(ids, 64, 48)
+    assert np.array_equal(t.offsets.cpu().numpy(), off)
+    assert int(t.ntiles.item()) == nt
+    assert np.array_equal(t.tile_row.cpu().numpy(), trow)
+    assert np.array_equal(t.tile_exp.cpu().numpy(), texp)
+
+
+# ------------------------------------------------------------ decode GEMV
+
+
+def test_quantized_matmul_cfg0(dev, orc):
+    say("quantized_matmul workload 0 [1,2048]x[4096,2048]")
+    wl = synth.make(0)
+    y = ops.quantized_matmul(bf16_t(wl["x"], dev), words_t(wl["w"], dev), bf16_t(wl["s"], dev),
+                             bf16_t(wl["b"], dev))
+    ref64, _ = orc.gather_qmm_rows(wl["x"], None, np.zeros(1, np.int32), wl["w"][None], wl["s"][None],
+                                   wl["b"][None])
+    assert_close_bf16(orc, bits(y), ref64, what="cfg0")
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 256, 512), (5, 192, 2560), (2, 64, 640), (1, 100, 128)])
+def test_quantized_matmul_shapes(dev, orc, M, N, K):
+    say(f"quantized_matmul M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 1000 + K)
+    w, s, b = synth.quant_weights(rng, (N,), K)
+    x = synth.bf16_bits(rng.normal(size=(M, K)).astype(np.float32))
+    y = ops.quantized_matmul(bf16_t(x, dev), words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    ref64, _ = orc.gather_qmm_rows(x, None, np.zeros(M, np.int32), w[None], s[None], b[None])
+    assert_close_bf16(orc, bits(y), ref64, what=f"qmm {M}x{N}x{K}")
+
+
+def test_gate_up_swiglu_cfg1(dev, orc):
+    say("gate_up + SwiGLU workload 1")
+    wl = synth.make(1)
+    h = ops.gate_up_silu(bf16_t(wl["x"], dev), words_t(wl["w"], dev), bf16_t(wl["s"], dev),
+                         bf16_t(wl["b"], dev), i32_t(wl["idx"], dev))
+    assert h.shape == (1, 10, 512)
+    gu64, _ = orc.gather_qmm_rows(wl["x"], np.zeros(10, np.int32), wl["idx"].reshape(-1), wl["w"],
+                                  wl["s"], wl["b"])
+    h64, _ = orc.swiglu(gu64)
+    assert_close_bf16(orc, bits(h).reshape(10, 512), h64, what="cfg1 swiglu")
+
+
+def test_gather_qmm_decode_form(dev, orc):
+    """x [T,1,1,K] with rhs [T,k] -> [T,k,1,N] (switch_layers.py:214 shapes)."""
+    say("gather_qmm decode form T=3 k=4")
+    rng = np.random.default_rng(21)
+    E, N, K, T, k = 16, 128, 1024, 3, 4
+    w, s, b = synth.quant_weights(rng, (E, N), K)
+    x = synth.bf16_bits(rng.normal(size=(T, 1, 1, K)).astype(np.float32))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    out = ops.gather_qmm(bf16_t(x, dev), words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev),
+                         rhs_indices=i32_t(idx, dev))
+    assert out.shape == (T, k, 1, N)
+    xr = np.repeat(np.arange(T), k).astype(np.int32)
+    ref64, _ = orc.gather_qmm_rows(x.reshape(T, K), xr, idx.reshape(-1), w, s, b)
+    assert_close_bf16(orc, bits(out).reshape(T * k, N), ref64, what="decode form")
+
+
+def test_down_wsum_cfg2(dev, orc):
+    say("down + weighted sum workload 2")
+    wl = synth.make(2)
+    y = ops.down_wsum(bf16_t(wl["h"], dev), words_t(wl["w"], dev), bf16_t(wl["s"], dev),
+                      bf16_t(wl["b"], dev), i32_t(wl["idx"], dev), f32_t(wl["scores"], dev))
+    y64, _ = orc.down_wsum(wl["h"], wl["idx"], wl["scores"], wl["w"], wl["s"], wl["b"])
+    assert_close_bf16(orc, bits(y), y64, what="cfg2 down+wsum")
+
+
+@pytest.mark.parametrize("T", [1, 3, 16])
+def test_down_wsum_widths(dev, orc, T):
+    say(f"down + weighted sum T={T}")
+    wl = synth.make(2, seed=100 + T, tokens=T, experts=64)
+    y = ops.down_wsum(bf16_t(wl["h"], dev), words_t(wl["w"], dev), bf16_t(wl["s"], dev),
+                      bf16_t(wl["b"], dev), i32_t(wl["idx"], dev), f32_t(wl["scores"], dev))
+    y64, _ = orc.down_wsum(wl["h"], wl["idx"], wl["scores"], wl["w"], wl["s"], wl["b"])
+    assert_close_bf16(orc, bits(y), y64, what=f"down T={T}")
+
+
+# ------------------------------------------------------------ weighted sum
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 256), (9, 256), (13, 2560), (128, 2560)])
+@pytest.mark.parametrize("sorted_layout", [True, False])
+@pytest.mark.parametrize("mode", ["clone", "ops", "fast"])
+def test_weighted_sum_bit_exact(dev, orc, rows, dim, sorted_layout, mode):
+    say(f"weighted_sum rows={rows} dim={dim} sorted={sorted_layout} mode={mode}")
+    rng = np.random.default_rng(rows * 7 + dim)
+    k = 10
+    xs = synth.bf16_bits(rng.normal(size=(rows * k, dim)).astype(np.float32))
+    sc = rng.uniform(size=(rows, k)).astype(np.float32)
+    sc /= sc.sum(-1, keepdims=True)
+    inv = rng.permutation(rows * k).astype(np.int32) if sorted_layout else None
+    got = ops.moe_weighted_sum(bf16_t(xs, dev), None if inv is None else i32_t(inv, dev), f32_t(sc, dev),
+                               (1, rows, dim), mode=mode)
+    ref = orc.weighted_sum(xs, inv, sc, rows, k, dim, mode)
+    assert np.array_equal(bits(got).reshape(rows, dim), ref)
+
+
+@pytest.mark.parametrize("k", [6, 8])
+def test_weighted_sum_other_top_k(dev, orc, k):
+    say(f"weighted_sum k={k}")
+    rng = np.random.default_rng(k)
+    rows, dim = 32, 512
+    xs = synth.bf16_bits(rng.normal(size=(rows * k, dim)).astype(np.float32))
+    sc = rng.uniform(size=(rows, k)).astype(np.float32)
+    inv = rng.permutation(rows * k).astype(np.int32)
+    got = ops.moe_weighted_sum(bf16_t(xs, dev), i32_t(inv, dev), f32_t(sc, dev), (1, rows, dim))
+    assert np.array_equal(bits(got).reshape(rows, dim), orc.weighted_sum(xs, inv, sc, rows, k, dim, "clone"))
+
+
+# ------------------------------------------------------------- prefill GEMM
+
+
+def _sorted_problem(seed, E, N, K, R, zipf=True, one_expert=False):
+    rng = np.random.default_rng(seed)
+    w, s, b = synth.quant_weights(rng, (E, N), K)
+    if one_expert:
+        ids = np.zeros(R, np.int32)
+    elif zipf:
+        p = 1.0 / np.arange(1, E + 1)
+        ids = np.sort(rng.choice(E, size=R, p=p / p.sum())).astype(np.int32)
+    else:
+        ids = np.sort(rng.integers(0, E, size=R)).astype(np.int32)
+    x = synth.bf16_bits(rng.normal(size=(R, K)).astype(np.float32))
+    return w, s, b, ids, x
+
+
+@pytest.mark.parametrize("E,N,K,R,kind", [
+    (8, 256, 1024, 300, "zipf"),
+    (32, 512, 2048, 700, "uniform"),
+    (4, 256, 1024, 500, "one"),
+    (16, 1024, 1024, 64, "zipf"),
+])
+def test_sorted_gemm_bf16(dev, orc, E, N, K, R, kind):
+    say(f"sorted GEMM E={E} N={N} K={K} R={R} {kind}")
+    w, s, b, ids, x = _sorted_problem(E * 31 + R, E, N, K, R, zipf=kind == "zipf", one_expert=kind == "one")
+    xt = bf16_t(x, dev)
+    tiles = ops.build_tiles(i32_t(ids, dev), E)
+    y = ops.gather_qmm_sorted(xt, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
+    got = bits(y)
+    ref_b64, _ = orc.gather_qmm_rows(x, None, ids, w, s, b, deq="bf16")
+    assert_close_bf16(orc, got, ref_b64, what=f"gemm bf16-deq {E}/{N}/{K}/{R}")
+    ref_e64, _ = orc.gather_qmm_rows(x, None, ids, w, s, b, deq="exact")
+    rep = orc.err_report(got, ref_e64)
+    print(f"[parity] vs exact-affine golden: {rep}", flush=True)
+    assert rep["rel_to_max"] <= 2.0 ** -8
+
+
+def test_gather_qmm_sorted_with_lhs_indices(dev, orc):
+    """The fused-gather form: x token-major, lhs_indices = order // k."""
+    say("gather_qmm sorted with lhs_indices")
+    wl = synth.make(3, seed=33, tokens=96, experts=16)
+    T, k = wl["idx"].shape
+    ids = wl["idx"].reshape(-1)
+    order = np.argsort(ids, kind="stable").astype(np.int32)
+    srt = ids[order]
+    lhs = (order // k).astype(np.int32)
+    x = wl["x"]
+    out = ops.gather_qmm(bf16_t(x, dev).reshape(T, 1, -1), words_t(wl["w"], dev), bf16_t(wl["s"], dev),
+                         bf16_t(wl["b"], dev), lhs_indices=i32_t(lhs, dev), rhs_indices=i32_t(srt, dev),
+                         sorted_indices=True)
+    assert out.shape == (T * k, 1, wl["w"].shape[1])
+    ref64, _ = orc.gather_qmm_rows(x, lhs, srt, wl["w"], wl["s"], wl["b"], deq="bf16")
+    assert_close_bf16(orc, bits(out).reshape(T * k, -1), ref64, what="lhs form")
+
+
+def _sample_rows(offsets, R, n_random, rng):
+    """Random rows plus the first and last row of every expert segment."""
+    edges = set()
+    for e in range(len(offsets) - 1):
+        if offsets[e + 1] > offsets[e]:
+            edges.add(int(offsets[e]))
+            edges.add(int(offsets[e + 1] - 1))
+            for j in range(offsets[e] + 127, offsets[e + 1], 128):
+                edges.update((int(j), int(j + 1) if j + 1 < offsets[e + 1] else int(j)))
+    rand = rng.choice(R, size=n_random, replace=False)
+    return np.array(sorted(edges | set(int(v) for v in rand)), np.int64)
+
+
+def test_sorted_gemm_cfg3_sampled(dev, orc):
+    say("sorted GEMM workload 3 (full size, sampled rows checked)")
+    wl = synth.make(3)
+    T, k = wl["idx"].shape
+    ids = wl["idx"]
+    x = bf16_t(wl["x"], dev)
+    r = ops.route(i32_t(ids, dev), 256)
+    lhs = torch.div(r.order, k, rounding_mode="floor").to(torch.int32)
+    y = ops.gather_qmm_sorted(x, words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev), r.tiles,
+                              x_rows=lhs)
+    torch.cuda.synchronize()
+    order, _, srt = orc.route_sort(ids, 256)
+    off = np.searchsorted(srt, np.arange(257), side="left")
+    rows = _sample_rows(off, T * k, 384, np.random.default_rng(0))
+    got = bits(y)[rows]
+    ref64, _ = orc.gather_qmm_rows(wl["x"], (order[rows] // k).astype(np.int32), srt[rows], wl["w"], wl["s"],
+                                   wl["b"], deq="bf16")
+    assert_close_bf16(orc, got, ref64, what=f"cfg3 {rows.size} rows")
+
+
+# -------------------------------------------------------------------- int8
+
+
+def test_quantize_act_int8_bit_exact(dev, orc):
+    say("int8 quantizer workload 4 activations")
+    wl = synth.make(4, tokens=512)
+    x = wl["x"].copy()
+    x[3] = 0  # an all-zero row
+    xi, sx = ops.quantize_act_int8(bf16_t(x, dev))
+    rxi, rsx = orc.quant_act_int8(x)
+    assert np.array_equal(sx.cpu().numpy().view(np.uint32), rsx.view(np.uint32))
+    assert np.array_equal(xi.cpu().numpy(), rxi)
+
+
+@pytest.mark.parametrize("E,N,K,R", [(8, 256, 1024, 300), (16, 512, 2048, 640)])
+def test_sorted_gemm_int8(dev, orc, E, N, K, R):
+    say(f"int8 sorted GEMM E={E} N={N} K={K} R={R}")
+    w, s, b, ids, x = _sorted_problem(E * 17 + R, E, N, K, R)
+    xi, sx = ops.quantize_act_int8(bf16_t(x, dev))
+    tiles = ops.build_tiles(i32_t(ids, dev), E)
+    y = ops.gather_qmm_int8_sorted(xi, sx, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
+    rxi, rsx = orc.quant_act_int8(x)
+    ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, None, ids, w, s, b)
+    assert_close_bf16(orc, bits(y), ref64, what=f"int8 gemm {E}/{N}/{K}/{R}")
+
+
+def test_sorted_gemm_int8_cfg4_sampled(dev, orc):
+    say("int8 sorted GEMM workload 4 (full size, sampled rows checked)")
+    wl = synth.make(4)
+    T, k = wl["idx"].shape
+    ids = wl["idx"]
+    xi, sx = ops.quantize_act_int8(bf16_t(wl["x"], dev))
+    r = ops.route(i32_t(ids, dev), 256)
+    lhs = torch.div(r.order, k, rounding_mode="floor").to(torch.int32)
+    y = ops.gather_qmm_int8_sorted(xi, sx, words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev),
+                                   r.tiles, x_rows=lhs)
+    torch.cuda.synchronize()
+    order, _, srt = orc.route_sort(ids, 256)
+    off = np.searchsorted(srt, np.arange(257), side="left")
+    rows = _sample_rows(off, T * k, 256, np.random.default_rng(1))
+    rxi, rsx = orc.quant_act_int8(wl["x"])
+    ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, (order[rows] // k).astype(np.int32), srt[rows], wl["w"],
+                                        wl["s"], wl["b"])
+    assert_close_bf16(orc, bits(y)[rows], ref64, what=f"cfg4 {rows.size} rows")

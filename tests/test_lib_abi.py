@@ -1,0 +1,82 @@
+"""The C-ABI library: builds, loads without a GPU, exports exactly what
+include/qmoe.h declares, and rejects bad arguments before touching the device."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from titan_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "qmoe.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(qmoe_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not _lib.LIB_PATH.exists():
+        from titan_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_bound_signatures():
+    assert declared() == sorted(_lib.SIGNATURES), (declared(), sorted(_lib.SIGNATURES))
+
+
+def test_every_declared_symbol_is_exported(L):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (qmoe_[a-z0-9_]+)$", out, flags=re.M))
+    missing = set(declared()) - exported
+    assert not missing, missing
+    for name in declared():
+        assert getattr(L, name) is not None
+
+
+def test_abi_version_matches_header(L):
+    m = re.search(r"#define QMOE_ABI_VERSION (\d+)", HEADER.read_text())
+    assert L.qmoe_abi_version() == int(m.group(1))
+
+
+def test_tile_rows_and_workspace_queries(L):
+    assert L.qmoe_gemm_tile_rows() == 128
+    ws = L.qmoe_route_workspace_size(40960, 256)
+    assert ws % 256 == 0 and ws >= 4 * (64 + 257 * 160)
+    assert L.qmoe_route_workspace_size(-1, 256) == 0
+
+
+def test_bad_arguments_are_rejected_without_a_device(L):
+    rc = L.qmoe_gather_qmv(None, None, None, 4, 2048, None, None, None, 8, 128, 64, 4, None, None)
+    assert rc == _lib.ERR_INVALID
+    assert "null" in _lib.last_error()
+    rc = L.qmoe_weighted_sum(None, None, None, 2, 0, 256, 2, None, None)
+    assert rc == _lib.ERR_INVALID
+
+
+def test_unsupported_configurations_say_so(L):
+    dummy = ctypes.c_void_p(16)  # never dereferenced: rejected on the host
+    rc = L.qmoe_gather_qmv(dummy, None, dummy, 4, 2048, dummy, dummy, dummy, 8, 128, 64, 8, dummy, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "bits=8" in _lib.last_error()
+    rc = L.qmoe_gather_qmv(dummy, None, dummy, 4, 2048, dummy, dummy, dummy, 8, 128, 48, 4, dummy, None)
+    assert rc == _lib.ERR_UNSUPPORTED
+    rc = L.qmoe_gather_qmm_sorted(dummy, None, 10, 2048, dummy, dummy, dummy, 8, 200, 64, 4, dummy, dummy,
+                                  dummy, dummy, 10, dummy, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "N=200" in _lib.last_error()
+    rc = L.qmoe_route(dummy, 10, 8, 128, dummy, dummy, dummy, dummy, dummy, dummy, dummy, 100, None, 0, None)
+    assert rc == _lib.ERR_WORKSPACE
+
+
+def test_check_maps_codes_to_exceptions(L):
+    with pytest.raises(_lib.QmoeUnsupported):
+        _lib.call("qmoe_weighted_sum", 16, None, 16, 2, 10, 256, 9, 16, None)
+    with pytest.raises(_lib.QmoeError):
+        _lib.call("qmoe_weighted_sum", None, None, None, 2, 10, 256, 2, None, None)

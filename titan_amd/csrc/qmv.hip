@@ -1,0 +1,343 @@
+// Decode-shape quantized matrix-vector kernels for gfx950.
+//
+// One weight row is reduced by a group of LPR lanes (LPR = 16 for K = 2048):
+// each lane owns NV chunks of 32 consecutive K elements, chunk v of lane l
+// starting at k = v*32*LPR + l*32, so the LPR lanes of a group read 256
+// contiguous bytes of packed codes per 16-byte load.  A wave holds 64/LPR
+// groups and therefore streams 64/LPR rows at once.
+//
+// Inner product without materialising bf16 weights:
+//   a code pair (q_a, q_b) becomes the bf16 pair (128 + q_a, 128 + q_b) by
+//   OR-ing 0x4300 into each half (0x4300 is 128.0; 128 + q is exact in bf16),
+//   v_dot2_f32_bf16 accumulates x*(128 + q) in fp32, and per 32-element chunk
+//       sum_k x*(s*q + b) = s*(dot - 128*sum_x) + b*sum_x.
+// This is the factored affine form of the reference decode kernels
+// (engine/patches/decode-fusion/fused_kernels.py:57-79), with the codes fed
+// to the dot unit two at a time.
+#include <stdarg.h>
+
+#include "common.h"
+
+namespace {
+
+constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
+
+// x pairs laid out to match the nibble pairs of one 32-bit code word:
+// word j covers elements 8j..8j+7; pairs are (0,4), (1,5), (2,6), (3,7).
+struct XChunk {
+  uint32_t p[16];
+  float sum;
+};
+
+__device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ src, XChunk& c) {
+  const uint4* q = reinterpret_cast<const uint4*>(src);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint4 a = q[j];
+    c.p[4 * j + 0] = (a.x & 0xFFFFu) | (a.z << 16);
+    c.p[4 * j + 1] = (a.x >> 16) | (a.z & 0xFFFF0000u);
+    c.p[4 * j + 2] = (a.y & 0xFFFFu) | (a.w << 16);
+    c.p[4 * j + 3] = (a.y >> 16) | (a.w & 0xFFFF0000u);
+    s += ((bf16lo(a.x) + bf16hi(a.x)) + (bf16lo(a.y) + bf16hi(a.y))) +
+         ((bf16lo(a.z) + bf16hi(a.z)) + (bf16lo(a.w) + bf16hi(a.w)));
+  }
+  c.sum = s;
+}
+
+// sum over the chunk of x*(128 + q)
+__device__ __forceinline__ float dot_chunk(const uint4& w, const XChunk& c) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t v = ws[j];
+    acc = dot2_bf16((v & 0x000F000Fu) | kMagic, c.p[4 * j + 0], acc);
+    acc = dot2_bf16(((v >> 4) & 0x000F000Fu) | kMagic, c.p[4 * j + 1], acc);
+    acc = dot2_bf16(((v >> 8) & 0x000F000Fu) | kMagic, c.p[4 * j + 2], acc);
+    acc = dot2_bf16(((v >> 12) & 0x000F000Fu) | kMagic, c.p[4 * j + 3], acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float affine_chunk(float dq, float xsum, float s, float b) {
+  return s * (dq - 128.0f * xsum) + b * xsum;
+}
+
+struct QmvArgs {
+  const uint16_t* x;
+  int64_t x_stride;      // elements between consecutive x rows
+  const int32_t* x_rows; // may be null
+  int64_t x_div;         // x row = pair / x_div when x_rows is null
+  const int32_t* experts;  // may be null (dense: expert 0)
+  int64_t n_pairs;
+  int K;
+  int group_size;
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  int num_experts;
+  int n_out;  // outputs per pair (N, or I for the SwiGLU form)
+  int n_w;    // weight rows per expert (N, or 2I)
+  uint16_t* out;
+};
+
+// MODE 0: out[r, n] = x_row . W[e][n]
+// MODE 1: out[r, i] = silu(x_row . W[e][i]) * (x_row . W[e][n_out + i])
+template <int NV, int LPR, int MODE>
+__global__ __launch_bounds__(64) void qmv_kernel(QmvArgs a) {
+  constexpr int GPW = 64 / LPR;
+  const int lane = threadIdx.x;
+  const int grp = lane / LPR;
+  const int l = lane % LPR;
+  const int64_t nblk = (a.n_out + GPW - 1) / GPW;
+  const int64_t r = blockIdx.x / nblk;
+  if (r >= a.n_pairs) return;
+  const int n = (int)(blockIdx.x % nblk) * GPW + grp;
+  const bool valid = n < a.n_out;
+  const int nn = valid ? n : 0;
+  int e = a.experts ? a.experts[r] : 0;
+  e = min(max(e, 0), a.num_experts - 1);
+  const int64_t xr = a.x_rows ? (int64_t)a.x_rows[r] : r / a.x_div;
+  const int K = a.K;
+  const int G = K / a.group_size;
+  const int64_t KW = K / 8;
+
+  const int64_t rg = (int64_t)e * a.n_w + nn;
+  const uint4* pg = reinterpret_cast<const uint4*>(a.w + rg * KW) + l;
+  uint4 wg[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) wg[v] = pg[v * LPR];
+  uint4 wu[MODE == 1 ? NV : 1];
+  const int64_t ru = rg + a.n_out;
+  if (MODE == 1) {
+    const uint4* pu = reinterpret_cast<const uint4*>(a.w + ru * KW) + l;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) wu[v] = pu[v * LPR];
+  }
+  float sg[NV], bg[NV], su[MODE == 1 ? NV : 1], bu[MODE == 1 ? NV : 1];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int g = (v * 32 * LPR + l * 32) / a.group_size;
+    sg[v] = bf16_to_f32(a.s[rg * G + g]);
+    bg[v] = bf16_to_f32(a.b[rg * G + g]);
+    if (MODE == 1) {
+      su[v] = bf16_to_f32(a.s[ru * G + g]);
+      bu[v] = bf16_to_f32(a.b[ru * G + g]);
+    }
+  }
+  const uint16_t* xrow = a.x + xr * a.x_stride;
+  XChunk xc[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) load_x_chunk(xrow + v * 32 * LPR + l * 32, xc[v]);
+
+  float accg = 0.f, accu = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    accg += affine_chunk(dot_chunk(wg[v], xc[v]), xc[v].sum, sg[v], bg[v]);
+    if (MODE == 1) accu += affine_chunk(dot_chunk(wu[v], xc[v]), xc[v].sum, su[v], bu[v]);
+  }
+  accg = group_sum<LPR>(accg);
+  if (MODE == 1) accu = group_sum<LPR>(accu);
+  if (l == 0 && valid) {
+    float o = accg;
+    if (MODE == 1) o = accg / (1.0f + expf(-accg)) * accu;
+    a.out[r * a.n_out + n] = (uint16_t)f32_to_bf16(o);
+  }
+}
+
+struct DownArgs {
+  const uint16_t* h;  // [T, k, I]
+  const int32_t* idx; // [T, k]
+  const float* scores;
+  int T, k, I, group_size;
+  const uint32_t* w;  // [E, D, I/8]
+  const uint16_t* s;
+  const uint16_t* b;
+  int num_experts, D;
+  uint16_t* y;  // [T, D]
+};
+
+// One block per group of 64/LPR output rows; wave t handles token t and walks
+// its k experts, folding the router score into the lane partial so a single
+// group reduction ends the row (fused_kernels.py:93-169 structure).  The
+// waves of a block read the same rows of whichever experts their tokens share.
+constexpr int kJB = 5;  // experts whose loads are issued together
+
+template <int NV, int LPR>
+__global__ __launch_bounds__(1024) void down_wsum_kernel(DownArgs a) {
+  constexpr int GPW = 64 / LPR;
+  const int t = threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  const int grp = lane / LPR;
+  const int l = lane % LPR;
+  const int d = blockIdx.x * GPW + grp;
+  const bool valid = d < a.D;
+  const int dd = valid ? d : 0;
+  const int I = a.I;
+  const int G = I / a.group_size;
+  const int64_t KW = I / 8;
+  float acc = 0.f;
+  for (int j0 = 0; j0 < a.k; j0 += kJB) {
+    uint4 wv[kJB][NV];
+    float sv[kJB][NV], bv[kJB][NV], sc[kJB];
+    int64_t prow[kJB];
+#pragma unroll
+    for (int jj = 0; jj < kJB; ++jj) {
+      const int j = min(j0 + jj, a.k - 1);
+      const int p = t * a.k + j;
+      int e = a.idx[p];
+      e = min(max(e, 0), a.num_experts - 1);
+      sc[jj] = (j0 + jj < a.k) ? a.scores[p] : 0.f;
+      prow[jj] = p;
+      const int64_t row = (int64_t)e * a.D + dd;
+      const uint4* pw = reinterpret_cast<const uint4*>(a.w + row * KW) + l;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        wv[jj][v] = pw[v * LPR];
+        const int g = (v * 32 * LPR + l * 32) / a.group_size;
+        sv[jj][v] = bf16_to_f32(a.s[row * G + g]);
+        bv[jj][v] = bf16_to_f32(a.b[row * G + g]);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < kJB; ++jj) {
+      if (j0 + jj >= a.k) break;  // uniform across the block
+      const uint16_t* hrow = a.h + prow[jj] * I;
+      float part = 0.f;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        XChunk hc;
+        load_x_chunk(hrow + v * 32 * LPR + l * 32, hc);
+        part += affine_chunk(dot_chunk(wv[jj][v], hc), hc.sum, sv[jj][v], bv[jj][v]);
+      }
+      acc += sc[jj] * part;
+    }
+  }
+  acc = group_sum<LPR>(acc);
+  if (l == 0 && valid) a.y[(int64_t)t * a.D + d] = (uint16_t)f32_to_bf16(acc);
+}
+
+// Pick lanes-per-row and chunks-per-lane for a reduction length K.
+bool pick_split(int64_t K, int* lpr, int* nv) {
+  if (K <= 0 || K % 32) return false;
+  const int64_t chunks = K / 32;
+  for (int L : {16, 8, 4}) {
+    if (chunks % L == 0 && chunks / L >= 1 && chunks / L <= 8) {
+      *lpr = L;
+      *nv = (int)(chunks / L);
+      return true;
+    }
+  }
+  return false;
+}
+
+template <int MODE>
+int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st) {
+  const int gpw = 64 / lpr;
+  const int64_t nblk = (a.n_out + gpw - 1) / gpw;
+  const int64_t blocks = a.n_pairs * nblk;
+  if (blocks <= 0) return QMOE_OK;
+  if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large (%lld blocks)", (long long)blocks);
+  dim3 grid((unsigned)blocks), block(64);
+#define QMV_CASE(NV_, L_) \
+  if (nv == NV_ && lpr == L_) { qmv_kernel<NV_, L_, MODE><<<grid, block, 0, st>>>(a); return qmoe::launch_status("qmv_kernel"); }
+#define QMV_NV(L_) QMV_CASE(1, L_) QMV_CASE(2, L_) QMV_CASE(3, L_) QMV_CASE(4, L_) \
+  QMV_CASE(5, L_) QMV_CASE(6, L_) QMV_CASE(7, L_) QMV_CASE(8, L_)
+  QMV_NV(16) QMV_NV(8) QMV_NV(4)
+#undef QMV_NV
+#undef QMV_CASE
+  return qmoe::fail(QMOE_ERR_UNSUPPORTED, "no qmv kernel for lpr=%d nv=%d", lpr, nv);
+}
+
+int check_common(int64_t K, int group_size, int bits, int* lpr, int* nv) {
+  if (bits != 4) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "bits=%d: only 4-bit codes have a kernel", bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "group_size=%d: kernels take 32, 64 or 128", group_size);
+  if (K % group_size) return qmoe::fail(QMOE_ERR_INVALID, "K=%lld not a multiple of group_size", (long long)K);
+  if (!pick_split(K, lpr, nv))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: needs K = 32*L*n, L in {4,8,16}, n <= 8", (long long)K);
+  return QMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int qmoe_gather_qmv(const uint16_t* x, const int32_t* x_rows, const int32_t* experts,
+                               int64_t n_rows, int64_t K, const uint32_t* w,
+                               const uint16_t* scales, const uint16_t* biases, int32_t num_experts,
+                               int64_t N, int group_size, int bits, uint16_t* out, void* stream) {
+  if (n_rows < 0 || N <= 0 || num_experts <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (n_rows == 0) return QMOE_OK;
+  if (!x || !experts || !w || !scales || !biases || !out) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  int lpr, nv;
+  int rc = check_common(K, group_size, bits, &lpr, &nv);
+  if (rc) return rc;
+  if (!qmoe::aligned16(x) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x and w must be 16-byte aligned");
+  if (N > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N too large");
+  QmvArgs a{x, K, x_rows, 1, experts, n_rows, (int)K, group_size, w, scales, biases, num_experts,
+            (int)N, (int)N, out};
+  return launch_qmv<0>(a, lpr, nv, qmoe::as_stream(stream));
+}
+
+extern "C" int qmoe_quantized_matmul(const uint16_t* x, int64_t M, int64_t K, const uint32_t* w,
+                                     const uint16_t* scales, const uint16_t* biases, int64_t N,
+                                     int group_size, int bits, uint16_t* out, void* stream) {
+  if (M < 0 || N <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (M == 0) return QMOE_OK;
+  if (!x || !w || !scales || !biases || !out) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  int lpr, nv;
+  int rc = check_common(K, group_size, bits, &lpr, &nv);
+  if (rc) return rc;
+  if (!qmoe::aligned16(x) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x and w must be 16-byte aligned");
+  if (N > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N too large");
+  QmvArgs a{x, K, nullptr, 1, nullptr, M, (int)K, group_size, w, scales, biases, 1, (int)N, (int)N, out};
+  return launch_qmv<0>(a, lpr, nv, qmoe::as_stream(stream));
+}
+
+extern "C" int qmoe_moe_gate_up_swiglu(const uint16_t* x, const int32_t* idx, int64_t T,
+                                       int64_t top_k, int64_t K, const uint32_t* w,
+                                       const uint16_t* scales, const uint16_t* biases,
+                                       int32_t num_experts, int64_t I, int group_size, int bits,
+                                       uint16_t* h, void* stream) {
+  if (T < 0 || top_k <= 0 || I <= 0 || num_experts <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (T == 0) return QMOE_OK;
+  if (!x || !idx || !w || !scales || !biases || !h) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  int lpr, nv;
+  int rc = check_common(K, group_size, bits, &lpr, &nv);
+  if (rc) return rc;
+  if (!qmoe::aligned16(x) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x and w must be 16-byte aligned");
+  if (I > 0x3FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "I too large");
+  QmvArgs a{x, K, nullptr, top_k, idx, T * top_k, (int)K, group_size, w, scales, biases, num_experts,
+            (int)I, (int)(2 * I), h};
+  return launch_qmv<1>(a, lpr, nv, qmoe::as_stream(stream));
+}
+
+extern "C" int qmoe_moe_down_wsum(const uint16_t* h, const int32_t* idx, const float* scores,
+                                  int64_t T, int64_t top_k, int64_t I, const uint32_t* w,
+                                  const uint16_t* scales, const uint16_t* biases,
+                                  int32_t num_experts, int64_t D, int group_size, int bits,
+                                  uint16_t* y, void* stream) {
+  if (T < 0 || top_k <= 0 || D <= 0 || num_experts <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (T == 0) return QMOE_OK;
+  if (!h || !idx || !scores || !w || !scales || !biases || !y) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (T > 16) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "T=%lld: the fused down kernel takes at most 16 tokens", (long long)T);
+  if (top_k > 64) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "top_k=%lld too large", (long long)top_k);
+  int lpr, nv;
+  int rc = check_common(I, group_size, bits, &lpr, &nv);
+  if (rc) return rc;
+  if (!qmoe::aligned16(h) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "h and w must be 16-byte aligned");
+  if (D > 0x3FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "D too large");
+  DownArgs a{h, idx, scores, (int)T, (int)top_k, (int)I, group_size, w, scales, biases,
+             num_experts, (int)D, y};
+  const int gpw = 64 / lpr;
+  dim3 grid((unsigned)((D + gpw - 1) / gpw)), block((unsigned)(64 * T));
+  hipStream_t st = qmoe::as_stream(stream);
+#define DW_CASE(NV_, L_) \
+  if (nv == NV_ && lpr == L_) { down_wsum_kernel<NV_, L_><<<grid, block, 0, st>>>(a); return qmoe::launch_status("down_wsum_kernel"); }
+#define DW_NV(L_) DW_CASE(1, L_) DW_CASE(2, L_) DW_CASE(3, L_) DW_CASE(4, L_) \
+  DW_CASE(5, L_) DW_CASE(6, L_) DW_CASE(7, L_) DW_CASE(8, L_)
+  DW_NV(16) DW_NV(8) DW_NV(4)
+#undef DW_NV
+#undef DW_CASE
+  return qmoe::fail(QMOE_ERR_UNSUPPORTED, "no down kernel for lpr=%d nv=%d", lpr, nv);
+}

@@ -1,0 +1,237 @@
+// Routing on the device: stable counting sort of expert ids, inverse
+// permutation, per-expert segment offsets and the ragged tile list.
+//
+// Replaces _gather_sort (switch_layers.py:13-18: two mx.argsort calls and a
+// gather) and the single-threadgroup tile walk of build_tiles
+// (titan/kernels/moe_gather_ws.py:133-156) with three launches:
+//   count   one block per CHUNK rows: per-chunk expert histogram in LDS
+//   scan    one block: expert-major exclusive scan of the histograms, which
+//           gives each (expert, chunk) its first output slot, the offsets,
+//           and the tile list
+//   scatter one wave per chunk: walks the chunk in row order 64 rows at a
+//           time; lanes holding the same id find each other with one ballot
+//           per id bit, so a row's slot is its chunk base plus the number of
+//           earlier rows with its id -- a stable sort with no atomics.
+#include "common.h"
+
+namespace {
+
+constexpr int kChunk = 256;
+constexpr int kScanThreads = 1024;
+
+__device__ __forceinline__ int clamp_id(int id, int E) { return id < 0 ? 0 : (id >= E ? E - 1 : id); }
+
+__global__ __launch_bounds__(256) void route_count_kernel(const int32_t* __restrict__ ids, int64_t n,
+                                                          int E, int nchunks, int32_t* __restrict__ counts) {
+  extern __shared__ int hist[];  // E + 1 (last slot: out-of-range ids)
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) hist[e] = 0;
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
+  if (i < n) {
+    const int id = ids[i];
+    if (id < 0 || id >= E) atomicAdd(&hist[E], 1);
+    atomicAdd(&hist[clamp_id(id, E)], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) counts[(int64_t)e * nchunks + blockIdx.x] = hist[e];
+}
+
+// Exclusive scan of one value per thread over the block; also returns the total.
+__device__ int block_exclusive_scan(int v, int* lds, int* total) {
+  const int tid = threadIdx.x;
+  lds[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < kScanThreads; off <<= 1) {
+    const int t = tid >= off ? lds[tid - off] : 0;
+    __syncthreads();
+    lds[tid] += t;
+    __syncthreads();
+  }
+  *total = lds[kScanThreads - 1];
+  const int incl = lds[tid];
+  __syncthreads();
+  return incl - v;
+}
+
+// Exclusive scan, in place, of a[0..L) with one block.
+__device__ int block_scan_array(int32_t* a, int64_t L, int* lds) {
+  const int tid = threadIdx.x;
+  const int64_t seg = (L + kScanThreads - 1) / kScanThreads;
+  const int64_t lo = min((int64_t)tid * seg, L), hi = min(lo + seg, L);
+  int local = 0;
+  for (int64_t i = lo; i < hi; ++i) local += a[i];
+  int total;
+  int run = block_exclusive_scan(local, lds, &total);
+  for (int64_t i = lo; i < hi; ++i) {
+    const int c = a[i];
+    a[i] = run;
+    run += c;
+  }
+  __syncthreads();
+  return total;
+}
+
+// Tiles from offsets (offsets[0..E] visible to the block): one (row_start,
+// expert) per tile_rows rows, expert-major; zero-fills [ntiles, max_tiles).
+__device__ void emit_tiles(const int32_t* offsets, int E, int tile_rows, int32_t* tile_row,
+                           int32_t* tile_exp, int32_t* ntiles, int64_t max_tiles, int* lds) {
+  const int tid = threadIdx.x;
+  const int seg = (E + kScanThreads - 1) / kScanThreads;
+  const int lo = min(tid * seg, E), hi = min(lo + seg, E);
+  int local = 0;
+  for (int e = lo; e < hi; ++e) local += (offsets[e + 1] - offsets[e] + tile_rows - 1) / tile_rows;
+  int total;
+  int64_t t = block_exclusive_scan(local, lds, &total);
+  for (int e = lo; e < hi; ++e) {
+    const int s = offsets[e], q = offsets[e + 1];
+    for (int r = s; r < q; r += tile_rows, ++t) {
+      if (t < max_tiles) {
+        tile_row[t] = r;
+        tile_exp[t] = e;
+      }
+    }
+  }
+  const int64_t nt = min((int64_t)total, max_tiles);
+  if (tid == 0) ntiles[0] = (int32_t)nt;
+  for (int64_t j = nt + tid; j < max_tiles; j += kScanThreads) {
+    tile_row[j] = 0;
+    tile_exp[j] = 0;
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int32_t* __restrict__ counts, int64_t n,
+                                                                  int E, int nchunks, int tile_rows,
+                                                                  int32_t* __restrict__ offsets,
+                                                                  int32_t* __restrict__ tile_row,
+                                                                  int32_t* __restrict__ tile_exp,
+                                                                  int32_t* __restrict__ ntiles,
+                                                                  int64_t max_tiles, int32_t* __restrict__ bad) {
+  __shared__ int lds[kScanThreads];
+  // out-of-range count: row E of the histogram table
+  int local = 0;
+  for (int c = threadIdx.x; c < nchunks; c += kScanThreads) local += counts[(int64_t)E * nchunks + c];
+  int nbad;
+  block_exclusive_scan(local, lds, &nbad);
+  if (threadIdx.x == 0) bad[0] = nbad;
+  block_scan_array(counts, (int64_t)E * nchunks, lds);
+  for (int e = threadIdx.x; e < E; e += kScanThreads) offsets[e] = nchunks ? counts[(int64_t)e * nchunks] : 0;
+  if (threadIdx.x == 0) offsets[E] = (int32_t)n;
+  __syncthreads();
+  emit_tiles(offsets, E, tile_rows, tile_row, tile_exp, ntiles, max_tiles, lds);
+}
+
+__global__ __launch_bounds__(64) void route_scatter_kernel(const int32_t* __restrict__ ids, int64_t n, int E,
+                                                           int nbits, int nchunks,
+                                                           const int32_t* __restrict__ base,
+                                                           int32_t* __restrict__ order,
+                                                           int32_t* __restrict__ inv_order,
+                                                           int32_t* __restrict__ sorted_ids) {
+  extern __shared__ int run[];  // E
+  const int lane = threadIdx.x;
+  const int c = blockIdx.x;
+  for (int e = lane; e < E; e += 64) run[e] = base[(int64_t)e * nchunks + c];
+  __syncthreads();
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int step = 0; step < kChunk / 64; ++step) {
+    const int64_t i = (int64_t)c * kChunk + step * 64 + lane;
+    const bool valid = i < n;
+    const int id = valid ? clamp_id(ids[i], E) : E;  // E: sentinel, never written
+    uint64_t m = __ballot(valid);
+    if (!valid) m = ~m;
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (id >> b) & 1;
+      const uint64_t bb = __ballot(bit);
+      m &= bit ? bb : ~bb;
+    }
+    const int rank = __popcll(m & lt);
+    if (valid) {
+      const int dst = run[id] + rank;
+      order[dst] = (int32_t)i;
+      sorted_ids[dst] = id;
+      inv_order[i] = dst;
+    }
+    __syncthreads();
+    if (valid && rank == 0) run[id] += __popcll(m);
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void tiles_from_sorted_kernel(const int32_t* __restrict__ sorted_ids,
+                                                                         int64_t n, int E, int tile_rows,
+                                                                         int32_t* __restrict__ offsets,
+                                                                         int32_t* __restrict__ tile_row,
+                                                                         int32_t* __restrict__ tile_exp,
+                                                                         int32_t* __restrict__ ntiles,
+                                                                         int64_t max_tiles) {
+  __shared__ int lds[kScanThreads];
+  for (int e = threadIdx.x; e <= E; e += kScanThreads) {
+    int64_t lo = 0, hi = n;  // first row whose id >= e
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (sorted_ids[mid] < e) lo = mid + 1;
+      else hi = mid;
+    }
+    offsets[e] = (int32_t)lo;
+  }
+  __syncthreads();
+  emit_tiles(offsets, E, tile_rows, tile_row, tile_exp, ntiles, max_tiles, lds);
+}
+
+int64_t n_chunks(int64_t n) { return (n + kChunk - 1) / kChunk; }
+
+}  // namespace
+
+extern "C" size_t qmoe_route_workspace_size(int64_t n_pairs, int32_t num_experts) {
+  if (n_pairs < 0 || num_experts <= 0) return 0;
+  const int64_t words = 64 + (int64_t)(num_experts + 1) * n_chunks(n_pairs);
+  return (size_t)(((words * 4) + 255) / 256 * 256);
+}
+
+extern "C" int qmoe_route(const int32_t* ids, int64_t n_pairs, int32_t num_experts, int32_t tile_rows,
+                          int32_t* order, int32_t* inv_order, int32_t* sorted_ids, int32_t* offsets,
+                          int32_t* tile_row, int32_t* tile_exp, int32_t* ntiles, int64_t max_tiles,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_pairs < 0 || num_experts <= 0 || tile_rows <= 0 || max_tiles < 0)
+    return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (num_experts > 8192) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "num_experts=%d > 8192", num_experts);
+  if (n_pairs > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "too many pairs");
+  if (!offsets || !tile_row || !tile_exp || !ntiles || (max_tiles == 0 && n_pairs > 0))
+    return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (n_pairs > 0 && (!ids || !order || !inv_order || !sorted_ids)) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  const size_t need = qmoe_route_workspace_size(n_pairs, num_experts);
+  if (!workspace || workspace_bytes < need)
+    return qmoe::fail(QMOE_ERR_WORKSPACE, "route needs %zu workspace bytes", need);
+  hipStream_t st = qmoe::as_stream(stream);
+  const int64_t nch = n_chunks(n_pairs);
+  int32_t* ws = static_cast<int32_t*>(workspace);
+  int32_t* bad = ws;
+  int32_t* counts = ws + 64;
+  if (nch > 0) {
+    route_count_kernel<<<dim3((unsigned)nch), dim3(kChunk), (num_experts + 1) * sizeof(int), st>>>(
+        ids, n_pairs, num_experts, (int)nch, counts);
+    int rc = qmoe::launch_status("route_count_kernel");
+    if (rc) return rc;
+  }
+  route_scan_kernel<<<dim3(1), dim3(kScanThreads), 0, st>>>(counts, n_pairs, num_experts, (int)nch, tile_rows,
+                                                            offsets, tile_row, tile_exp, ntiles, max_tiles, bad);
+  int rc = qmoe::launch_status("route_scan_kernel");
+  if (rc || nch == 0) return rc;
+  int nbits = 1;
+  while ((1 << nbits) <= num_experts) ++nbits;  // ids in [0, E] (E is the sentinel)
+  route_scatter_kernel<<<dim3((unsigned)nch), dim3(64), num_experts * sizeof(int), st>>>(
+      ids, n_pairs, num_experts, nbits, (int)nch, counts, order, inv_order, sorted_ids);
+  return qmoe::launch_status("route_scatter_kernel");
+}
+
+extern "C" int qmoe_build_tiles(const int32_t* sorted_ids, int64_t n_rows, int32_t num_experts,
+                                int32_t tile_rows, int32_t* offsets, int32_t* tile_row, int32_t* tile_exp,
+                                int32_t* ntiles, int64_t max_tiles, void* stream) {
+  if (n_rows < 0 || num_experts <= 0 || tile_rows <= 0 || max_tiles < 0)
+    return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (n_rows > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "too many rows");
+  if (!offsets || !tile_row || !tile_exp || !ntiles || (n_rows > 0 && !sorted_ids))
+    return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  tiles_from_sorted_kernel<<<dim3(1), dim3(kScanThreads), 0, qmoe::as_stream(stream)>>>(
+      sorted_ids, n_rows, num_experts, tile_rows, offsets, tile_row, tile_exp, ntiles, max_tiles);
+  return qmoe::launch_status("tiles_from_sorted_kernel");
+}

@@ -1,0 +1,100 @@
+// Un-permute + router-weighted top-k sum (titan/kernels/moe_weighted_sum.py:44-98).
+//
+// Each thread owns 8 adjacent columns of one output row and walks the k
+// expert outputs in order, keeping eight partial sums per column (slot j mod 8)
+// that are combined in slot order at the end.  The arithmetic is spelled out
+// with contraction switched off so no multiply-add is fused: every mode is a
+// fixed sequence of IEEE operations and bf16 roundings, bit-for-bit
+// reproducible against a CPU restatement of the same sequence.
+#include "common.h"
+
+namespace {
+
+template <int MODE>  // QMOE_WSUM_FAST, _OPS, _CLONE
+__global__ __launch_bounds__(256) void wsum_kernel(const uint16_t* __restrict__ xs,
+                                                   const int32_t* __restrict__ inv,
+                                                   const float* __restrict__ scores, int64_t rows, int k,
+                                                   int64_t dim, uint16_t* __restrict__ out) {
+#pragma clang fp contract(off)
+  constexpr bool kRoundProd = MODE >= QMOE_WSUM_OPS;
+  constexpr bool kBfAcc = MODE == QMOE_WSUM_CLONE;
+  const int64_t c8 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  const int64_t r = blockIdx.y;
+  if (c8 >= dim || r >= rows) return;
+  float acc[8][8];
+#pragma unroll
+  for (int a = 0; a < 8; ++a)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) acc[a][v] = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const int64_t p = r * k + j;
+    const int64_t src = inv ? (int64_t)inv[p] : p;
+    float s = scores[p];
+    if (MODE >= QMOE_WSUM_OPS) s = round_bf16(s);
+    const uint4 q = *reinterpret_cast<const uint4*>(xs + src * dim + c8);
+    const uint32_t pr[4] = {q.x, q.y, q.z, q.w};
+    const int slot = j & 7;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const float xv = (v & 1) ? bf16hi(pr[v >> 1]) : bf16lo(pr[v >> 1]);
+      float prod = s * xv;
+      if (kRoundProd) prod = round_bf16(prod);
+      // slot is dynamic; select it with a fully unrolled compare so acc stays in registers
+#pragma unroll
+      for (int a = 0; a < 8; ++a) {
+        if (a == slot) {
+          float t = acc[a][v] + prod;
+          acc[a][v] = kBfAcc ? round_bf16(t) : t;
+        }
+      }
+    }
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int v = 0; v < 8; v += 2) {
+    float r0 = acc[0][v], r1 = acc[0][v + 1];
+#pragma unroll
+    for (int a = 1; a < 8; ++a) {
+      r0 = r0 + acc[a][v];
+      r1 = r1 + acc[a][v + 1];
+      if (kBfAcc) {
+        r0 = round_bf16(r0);
+        r1 = round_bf16(r1);
+      }
+    }
+    o[v >> 1] = pack_bf16x2(r0, r1);
+  }
+  *reinterpret_cast<uint4*>(out + r * dim + c8) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+}  // namespace
+
+extern "C" int qmoe_weighted_sum(const uint16_t* xs, const int32_t* inv_order, const float* scores,
+                                 int64_t rows, int64_t top_k, int64_t dim, int mode, uint16_t* out,
+                                 void* stream) {
+  if (rows < 0 || top_k <= 0 || dim <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (rows == 0) return QMOE_OK;
+  if (!xs || !scores || !out) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (mode < QMOE_WSUM_FAST || mode > QMOE_WSUM_CLONE) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "mode=%d", mode);
+  if (dim % 8) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "dim=%lld: must be a multiple of 8", (long long)dim);
+  if (!qmoe::aligned16(xs) || !qmoe::aligned16(out))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "xs and out must be 16-byte aligned");
+  if (rows > 65535) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "rows=%lld > 65535", (long long)rows);
+  if (top_k > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_INVALID, "top_k too large");
+  const int64_t threads = dim / 8;
+  dim3 block((unsigned)(threads < 256 ? threads : 256));
+  dim3 grid((unsigned)((threads + block.x - 1) / block.x), (unsigned)rows);
+  hipStream_t st = qmoe::as_stream(stream);
+  switch (mode) {
+    case QMOE_WSUM_FAST:
+      wsum_kernel<QMOE_WSUM_FAST><<<grid, block, 0, st>>>(xs, inv_order, scores, rows, (int)top_k, dim, out);
+      break;
+    case QMOE_WSUM_OPS:
+      wsum_kernel<QMOE_WSUM_OPS><<<grid, block, 0, st>>>(xs, inv_order, scores, rows, (int)top_k, dim, out);
+      break;
+    default:
+      wsum_kernel<QMOE_WSUM_CLONE><<<grid, block, 0, st>>>(xs, inv_order, scores, rows, (int)top_k, dim, out);
+      break;
+  }
+  return qmoe::launch_status("wsum_kernel");
+}

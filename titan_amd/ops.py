@@ -1,0 +1,451 @@
+"""Torch-facing wrappers of the libqmoe C ABI.
+
+Tensors are ROCm torch tensors: bf16 activations, packed weights as ``int32``
+or ``uint32`` (the bits are what matter), bf16 scales and biases.  Every
+function enqueues on torch's current stream and never synchronises.  Each
+raises :class:`~titan_amd._lib.QmoeUnsupported` for a configuration without a
+kernel and :class:`~titan_amd._lib.QmoeLibraryMissing` when the library is not
+built: there is no other implementation behind these names.
+
+Call-surface parity with the reference (paths relative to its root):
+
+* :func:`gather_qmm`            mx.gather_qmm as called at
+  titan/adapters/mlx/vendor/mlx_lm/models/switch_layers.py:87-98
+* :func:`quantized_matmul`      mx.quantized_matmul (titan/adapters/mlx/compiled.py:209-218)
+* :func:`route` / :func:`build_tiles`   _gather_sort (switch_layers.py:13-18) and
+  titan/kernels/moe_gather_ws.py:181-202
+* :func:`moe_weighted_sum`      titan/kernels/moe_weighted_sum.py:142-195
+* :func:`gate_up_silu` / :func:`down_wsum`
+  engine/patches/decode-fusion/fused_kernels.py:194-231
+* :func:`quantize_act_int8` / :func:`gather_qmm_int8`
+  titan/kernels/moe_gather_int8.py:168-182, 393-425
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import QmoeError, QmoeUnsupported
+
+GROUP = 64
+BITS = 4
+# SwitchGLU sorts when indices.size >= 64 (switch_layers.py:218); the grouped
+# GEMM takes sorted calls from that size up.
+SORTED_MIN_ROWS = 64
+
+
+def tile_rows() -> int:
+    """Rows per tile of the grouped GEMM (the tile table must use this)."""
+    return int(_lib.load().qmoe_gemm_tile_rows())
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"{name} is on {t.device}; libqmoe runs on the GPU")
+
+
+def _ready(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous and 16-byte aligned (a copy only when it is not)."""
+    if not t.is_contiguous():
+        t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _bf16(t: torch.Tensor, name: str) -> torch.Tensor:
+    _dev(t, name)
+    if t.dtype != torch.bfloat16:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"{name} must be bfloat16, got {t.dtype}")
+    return _ready(t)
+
+
+def _words(t: torch.Tensor, name: str) -> torch.Tensor:
+    _dev(t, name)
+    if t.dtype not in (torch.int32, torch.uint32):
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"{name} must hold packed uint32 words, got {t.dtype}")
+    return _ready(t)
+
+
+def _i32(t: torch.Tensor, name: str, device) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        t = torch.as_tensor(t)
+    if t.device != device:
+        t = t.to(device)
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return _ready(t)
+
+
+def _f32(t: torch.Tensor, name: str, device) -> torch.Tensor:
+    if t.device != device:
+        t = t.to(device)
+    if t.dtype != torch.float32:
+        t = t.to(torch.float32)
+    return _ready(t)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------------ layout
+
+
+def unpack(w: torch.Tensor, bits: int = BITS) -> torch.Tensor:
+    """uint8 codes [..., words * 32/bits], low bits first."""
+    w = _words(w, "w")
+    per = 32 // bits
+    out = torch.empty(*w.shape[:-1], w.shape[-1] * per, dtype=torch.uint8, device=w.device)
+    _lib.call("qmoe_unpack", w.data_ptr(), w.numel(), bits, out.data_ptr(), _stream(w))
+    return out
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = GROUP,
+               bits: int = BITS) -> torch.Tensor:
+    """bf16_rne(fmaf(q, s, b)) for every element (mx.dequantize)."""
+    w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    K = w.shape[-1] * 32 // bits
+    rows = w.numel() // w.shape[-1]
+    out = torch.empty(*w.shape[:-1], K, dtype=torch.bfloat16, device=w.device)
+    _lib.call("qmoe_dequantize", w.data_ptr(), scales.data_ptr(), biases.data_ptr(), rows, K,
+              group_size, bits, out.data_ptr(), _stream(w))
+    return out
+
+
+# ------------------------------------------------------------------ routing
+
+
+def max_tiles(rows: int, num_experts: int, tile_rows_: int) -> int:
+    """Static bound on sum(ceil(rows_e / tile_rows)) (moe_gather_ws.py:176-178)."""
+    return (rows + tile_rows_ - 1) // tile_rows_ + num_experts
+
+
+@dataclass(frozen=True)
+class TileTable:
+    """Segment offsets plus the ragged (row_start, expert) tile list, built on
+    the device and owned by the caller (moe_gather_ws.py:159-173)."""
+
+    offsets: torch.Tensor   # [E + 1] int32
+    tile_row: torch.Tensor  # [maxt] int32
+    tile_exp: torch.Tensor  # [maxt] int32
+    ntiles: torch.Tensor    # [1] int32
+    maxt: int
+    tile_rows: int
+    num_experts: int
+    rows: int
+
+
+@dataclass(frozen=True)
+class Routing:
+    """Stable expert sort of flattened (token, slot) pairs plus its tile table."""
+
+    order: torch.Tensor       # [n] pair index of sorted row i
+    inv_order: torch.Tensor   # [n] argsort(order)
+    sorted_ids: torch.Tensor  # [n] ids[order]
+    tiles: TileTable
+    bad_ids: torch.Tensor     # [1] int32 count of ids outside [0, E) (clamped)
+
+
+def build_tiles(sorted_ids: torch.Tensor, num_experts: int, tile_rows_: int | None = None) -> TileTable:
+    """Tile table over ids already sorted ascending."""
+    _dev(sorted_ids, "sorted_ids")
+    dev = sorted_ids.device
+    ids = _i32(sorted_ids.reshape(-1), "sorted_ids", dev)
+    tr = tile_rows() if tile_rows_ is None else int(tile_rows_)
+    n = ids.numel()
+    mt = max_tiles(n, num_experts, tr)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    trow = torch.empty(mt, dtype=torch.int32, device=dev)
+    texp = torch.empty(mt, dtype=torch.int32, device=dev)
+    nt = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.call("qmoe_build_tiles", ids.data_ptr(), n, num_experts, tr, offsets.data_ptr(),
+              trow.data_ptr(), texp.data_ptr(), nt.data_ptr(), mt, _stream(ids))
+    return TileTable(offsets, trow, texp, nt, mt, tr, num_experts, n)
+
+
+def route(ids: torch.Tensor, num_experts: int, tile_rows_: int | None = None) -> Routing:
+    """Stable argsort of expert ids with inverse and tile table, no host sync."""
+    _dev(ids, "ids")
+    dev = ids.device
+    flat = _i32(ids.reshape(-1), "ids", dev)
+    n = flat.numel()
+    tr = tile_rows() if tile_rows_ is None else int(tile_rows_)
+    mt = max_tiles(n, num_experts, tr)
+    L = _lib.load()
+    ws_bytes = int(L.qmoe_route_workspace_size(n, num_experts))
+    ws = torch.empty(max(ws_bytes, 256) // 4, dtype=torch.int32, device=dev)
+    order = torch.empty(n, dtype=torch.int32, device=dev)
+    inv = torch.empty(n, dtype=torch.int32, device=dev)
+    srt = torch.empty(n, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    trow = torch.empty(mt, dtype=torch.int32, device=dev)
+    texp = torch.empty(mt, dtype=torch.int32, device=dev)
+    nt = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.call("qmoe_route", flat.data_ptr(), n, num_experts, tr, order.data_ptr(), inv.data_ptr(),
+              srt.data_ptr(), offsets.data_ptr(), trow.data_ptr(), texp.data_ptr(), nt.data_ptr(), mt,
+              ws.data_ptr(), ws.numel() * 4, _stream(flat))
+    tiles = TileTable(offsets, trow, texp, nt, mt, tr, num_experts, n)
+    return Routing(order, inv, srt, tiles, ws[:1])
+
+
+# ------------------------------------------------------------- gather_qmm
+
+
+def _check_quant(w, scales, group_size, bits, K):
+    if bits not in (4, 8):
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"bits={bits}")
+    if w.shape[-1] * 32 // bits != K:
+        raise ValueError(f"x has K={K} but w packs {w.shape[-1] * 32 // bits} elements per row")
+    if scales.shape[-1] * group_size != K:
+        raise ValueError(f"scales carry {scales.shape[-1]} groups of {group_size}, K={K}")
+
+
+def gather_qmv(x: torch.Tensor, x_rows: torch.Tensor | None, experts: torch.Tensor, w: torch.Tensor,
+               scales: torch.Tensor, biases: torch.Tensor, group_size: int = GROUP,
+               bits: int = BITS) -> torch.Tensor:
+    """Row form, matrix-vector kernel: out[r] = x[x_rows[r]] @ deq(W[experts[r]])^T."""
+    x = _bf16(x, "x")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    _check_quant(w, scales, group_size, bits, K)
+    dev = x.device
+    e = _i32(experts.reshape(-1), "experts", dev)
+    xr = None if x_rows is None else _i32(x_rows.reshape(-1), "x_rows", dev)
+    E, N = w.shape[0], w.shape[1]
+    out = torch.empty(e.numel(), N, dtype=torch.bfloat16, device=dev)
+    _lib.call("qmoe_gather_qmv", x2.data_ptr(), _ptr(xr), e.data_ptr(), e.numel(), K, w.data_ptr(),
+              scales.data_ptr(), biases.data_ptr(), E, N, group_size, bits, out.data_ptr(), _stream(x))
+    return out
+
+
+def gather_qmm_sorted(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                      tiles: TileTable, x_rows: torch.Tensor | None = None, group_size: int = GROUP,
+                      bits: int = BITS) -> torch.Tensor:
+    """Grouped GEMM over expert-sorted rows described by ``tiles``:
+    out[r] = x[x_rows[r]] @ deq(W[e(r)])^T, rows [0, tiles.rows)."""
+    x = _bf16(x, "x")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    _check_quant(w, scales, group_size, bits, K)
+    dev = x.device
+    xr = None if x_rows is None else _i32(x_rows.reshape(-1), "x_rows", dev)
+    R = tiles.rows
+    E, N = w.shape[0], w.shape[1]
+    if tiles.num_experts != E:
+        raise ValueError("tile table was built for a different expert count")
+    if tiles.tile_rows != tile_rows():
+        raise ValueError(f"tile table uses {tiles.tile_rows} rows per tile, the GEMM needs {tile_rows()}")
+    out = torch.empty(R, N, dtype=torch.bfloat16, device=dev)
+    _lib.call("qmoe_gather_qmm_sorted", x2.data_ptr(), _ptr(xr), R, K, w.data_ptr(), scales.data_ptr(),
+              biases.data_ptr(), E, N, group_size, bits, tiles.offsets.data_ptr(),
+              tiles.tile_row.data_ptr(), tiles.tile_exp.data_ptr(), tiles.ntiles.data_ptr(), tiles.maxt,
+              out.data_ptr(), _stream(x))
+    return out
+
+
+def gemm_supported(K: int, N: int, group_size: int, bits: int) -> bool:
+    return bits == 4 and group_size == 64 and K % 1024 == 0 and N % 256 == 0
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None = None,
+               lhs_indices: torch.Tensor | None = None, rhs_indices: torch.Tensor | None = None,
+               transpose: bool = True, group_size: int = GROUP, bits: int = BITS, mode: str = "affine",
+               sorted_indices: bool = False, *, tiles: TileTable | None = None) -> torch.Tensor:
+    """mx.gather_qmm for transpose=True affine weights.
+
+    ``x`` is [..., M, K] and ``w`` [E, N, K*bits/32].  The batch is the
+    broadcast of ``lhs_indices`` (default: x's own batch) with ``rhs_indices``
+    (default: every expert), and the result is [*batch, M, N]:
+    out[i, m] = x[lhs[i], m] @ deq(W[rhs[i]])^T.  ``sorted_indices`` promises
+    ascending ``rhs_indices`` and selects the grouped GEMM for 64 rows or more.
+    """
+    if mode != "affine":
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"mode={mode!r}: only affine quantization")
+    if not transpose:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, "transpose=False")
+    if biases is None:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, "affine weights need biases")
+    if w.dim() != 3:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"w must be [E, N, K*bits/32], got {tuple(w.shape)}")
+    x = _bf16(x, "x")
+    dev = x.device
+    if x.dim() < 2:
+        raise ValueError("x must be at least 2-D ([..., M, K])")
+    M, K = x.shape[-2], x.shape[-1]
+    xb = tuple(x.shape[:-2])
+    E = w.shape[0]
+    rhs = torch.arange(E, device=dev, dtype=torch.int32) if rhs_indices is None else rhs_indices.to(dev)
+    if lhs_indices is None:
+        batch = torch.broadcast_shapes(xb, tuple(rhs.shape))
+        nxb = math.prod(xb)
+        xidx = torch.arange(nxb, device=dev, dtype=torch.int32).reshape(xb).expand(batch).reshape(-1)
+        identity_x = xb == tuple(batch)
+    else:
+        lhs = lhs_indices.to(dev)
+        batch = torch.broadcast_shapes(tuple(lhs.shape), tuple(rhs.shape))
+        xidx = lhs.to(torch.int32).expand(batch).reshape(-1)
+        identity_x = False
+    e = rhs.to(torch.int32).expand(batch).reshape(-1)
+    if M == 1:
+        x_rows, experts = xidx, e
+    else:
+        ar = torch.arange(M, device=dev, dtype=torch.int32)
+        x_rows = (xidx[:, None] * M + ar[None, :]).reshape(-1)
+        experts = e.repeat_interleave(M)
+    n_rows = experts.numel()
+    N = w.shape[1]
+    if n_rows == 0:
+        return torch.empty(*batch, M, N, dtype=torch.bfloat16, device=dev)
+    xr = None if identity_x else x_rows
+    if sorted_indices and n_rows >= SORTED_MIN_ROWS and gemm_supported(K, N, group_size, bits):
+        if tiles is None or tiles.rows != n_rows:
+            tiles = build_tiles(experts, E)
+        out = gather_qmm_sorted(x, w, scales, biases, tiles, xr, group_size, bits)
+    else:
+        out = gather_qmv(x, xr, experts, w, scales, biases, group_size, bits)
+    return out.reshape(*batch, M, N)
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                     transpose: bool = True, group_size: int = GROUP, bits: int = BITS,
+                     mode: str = "affine") -> torch.Tensor:
+    """mx.quantized_matmul for transpose=True affine weights: x[..., K] @ deq(W)^T."""
+    if mode != "affine":
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"mode={mode!r}")
+    if not transpose:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, "transpose=False")
+    x = _bf16(x, "x")
+    w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    if w.dim() != 2:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"w must be [N, K*bits/32], got {tuple(w.shape)}")
+    K = x.shape[-1]
+    _check_quant(w, scales, group_size, bits, K)
+    N = w.shape[0]
+    M = x.numel() // K
+    out = torch.empty(*x.shape[:-1], N, dtype=torch.bfloat16, device=x.device)
+    _lib.call("qmoe_quantized_matmul", x.data_ptr(), M, K, w.data_ptr(), scales.data_ptr(),
+              biases.data_ptr(), N, group_size, bits, out.data_ptr(), _stream(x))
+    return out
+
+
+# ------------------------------------------------------------ fused decode
+
+
+def gate_up_silu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 idx: torch.Tensor, group_size: int = GROUP, bits: int = BITS) -> torch.Tensor:
+    """x [T, K], fused gate_up W [E, 2I, K*bits/32] (gate rows first), idx [T, k]
+    -> h [T, k, I] = silu(gate) * up, fp32 until the bf16 store."""
+    x = _bf16(x, "x")
+    w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    T, K = x.shape
+    _check_quant(w, scales, group_size, bits, K)
+    idx = _i32(idx, "idx", x.device)
+    k = idx.shape[-1]
+    E, two_i = w.shape[0], w.shape[1]
+    I = two_i // 2
+    h = torch.empty(T, k, I, dtype=torch.bfloat16, device=x.device)
+    _lib.call("qmoe_moe_gate_up_swiglu", x.data_ptr(), idx.data_ptr(), T, k, K, w.data_ptr(),
+              scales.data_ptr(), biases.data_ptr(), E, I, group_size, bits, h.data_ptr(), _stream(x))
+    return h
+
+
+def down_wsum(h: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+              idx: torch.Tensor, scores: torch.Tensor, group_size: int = GROUP,
+              bits: int = BITS) -> torch.Tensor:
+    """h [T, k, I], down W [E, D, I*bits/32], idx [T, k], scores [T, k]
+    -> y [T, D] = sum_j scores[t, j] * W[idx[t, j]] @ h[t, j]."""
+    h = _bf16(h, "h")
+    w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    T, k, I = h.shape
+    _check_quant(w, scales, group_size, bits, I)
+    idx = _i32(idx, "idx", h.device)
+    sc = _f32(scores, "scores", h.device)
+    E, D = w.shape[0], w.shape[1]
+    y = torch.empty(T, D, dtype=torch.bfloat16, device=h.device)
+    _lib.call("qmoe_moe_down_wsum", h.data_ptr(), idx.data_ptr(), sc.data_ptr(), T, k, I, w.data_ptr(),
+              scales.data_ptr(), biases.data_ptr(), E, D, group_size, bits, y.data_ptr(), _stream(h))
+    return y
+
+
+# ------------------------------------------------------------ weighted sum
+
+
+def moe_weighted_sum(xs: torch.Tensor, inv_order: torch.Tensor | None, scores: torch.Tensor,
+                     out_shape, mode: str = "clone") -> torch.Tensor:
+    """Un-permute + router-weighted top-k sum (moe_weighted_sum.py:142-195).
+
+    ``xs`` flattens to [R*k, D]; ``inv_order`` is the [R*k] permutation from
+    the sort or None for token-major input; ``scores`` is [..., k]."""
+    if mode not in _lib.WSUM_MODES:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"mode={mode!r}")
+    xs = _bf16(xs, "xs")
+    dim = int(out_shape[-1])
+    rows = math.prod(int(d) for d in out_shape[:-1])
+    k = scores.shape[-1]
+    xs2 = xs.reshape(rows * k, dim)
+    sc = _f32(scores.reshape(rows * k), "scores", xs.device)
+    inv = None if inv_order is None else _i32(inv_order.reshape(-1), "inv_order", xs.device)
+    out = torch.empty(*out_shape, dtype=torch.bfloat16, device=xs.device)
+    _lib.call("qmoe_weighted_sum", xs2.data_ptr(), _ptr(inv), sc.data_ptr(), rows, k, dim,
+              _lib.WSUM_MODES[mode], out.data_ptr(), _stream(xs))
+    return out
+
+
+# -------------------------------------------------------------------- int8
+
+
+def quantize_act_int8(x: torch.Tensor):
+    """Per-token symmetric int8: (xi int8 [R, K], sx float32 [R])."""
+    x = _bf16(x, "x")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    R = x2.shape[0]
+    xi = torch.empty(R, K, dtype=torch.int8, device=x.device)
+    sx = torch.empty(R, dtype=torch.float32, device=x.device)
+    _lib.call("qmoe_quantize_act_int8", x2.data_ptr(), R, K, xi.data_ptr(), sx.data_ptr(), _stream(x))
+    return xi, sx
+
+
+def gather_qmm_int8_sorted(xi: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                           biases: torch.Tensor, tiles: TileTable, x_rows: torch.Tensor | None = None,
+                           group_size: int = GROUP, bits: int = BITS) -> torch.Tensor:
+    """int8-activation x int4-weight grouped GEMM over expert-sorted rows."""
+    _dev(xi, "xi")
+    if xi.dtype != torch.int8:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"xi must be int8, got {xi.dtype}")
+    xi = _ready(xi)
+    sx = _f32(sx, "sx", xi.device)
+    K = xi.shape[-1]
+    w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    _check_quant(w, scales, group_size, bits, K)
+    xr = None if x_rows is None else _i32(x_rows.reshape(-1), "x_rows", xi.device)
+    E, N = w.shape[0], w.shape[1]
+    if tiles.num_experts != E or tiles.tile_rows != tile_rows():
+        raise ValueError("tile table does not match this call")
+    out = torch.empty(tiles.rows, N, dtype=torch.bfloat16, device=xi.device)
+    _lib.call("qmoe_gather_qmm_int8_sorted", xi.data_ptr(), sx.data_ptr(), _ptr(xr), tiles.rows, K,
+              w.data_ptr(), scales.data_ptr(), biases.data_ptr(), E, N, group_size, bits,
+              tiles.offsets.data_ptr(), tiles.tile_row.data_ptr(), tiles.tile_exp.data_ptr(),
+              tiles.ntiles.data_ptr(), tiles.maxt, out.data_ptr(), _stream(xi))
+    return out
+
+
+__all__ = [
+    "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "Routing", "build_tiles", "route",
+    "max_tiles", "tile_rows", "unpack", "dequantize", "gather_qmv", "gather_qmm_sorted", "gather_qmm",
+    "gemm_supported", "quantized_matmul", "gate_up_silu", "down_wsum", "moe_weighted_sum",
+    "quantize_act_int8", "gather_qmm_int8_sorted",
+]
