@@ -44,7 +44,9 @@ def parse():
     ap.add_argument("--rotate-gb", type=float, default=1.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default=None, help="run one workload's timed loop only (for profiling)")
+    ap.add_argument("--only", default=None,
+                    help="run one workload's timed loop only, or 'copy' for the calibration copy kernel")
+    ap.add_argument("--eager", action="store_true", help="launch the timed steps eagerly (no graph)")
     return ap.parse_args()
 
 
@@ -94,6 +96,37 @@ def weight_sets(wl, n_sets, dev, seed):
 def n_sets_for(wl, rotate_gb):
     per = wl["w"].nbytes + wl["s"].nbytes + wl["b"].nbytes
     return max(1, int(np.ceil(rotate_gb * 1e9 / per)))
+
+
+def time_eager(fn_list, warmup, dev):
+    """Eager launches (used under counter collection)."""
+    import torch
+
+    for i in range(warmup):
+        fn_list[i % len(fn_list)]()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    st = torch.cuda.current_stream()
+    e0.record(st)
+    for fn in fn_list:
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / len(fn_list), None
+
+
+def calibration_copy(dev, mib=256, reps=5):
+    """A plain device copy of known size: the scale for HBM byte counters."""
+    import torch
+
+    n = mib * 2 ** 20 // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes_read": n * 4, "bytes_written": n * 4, "reps": reps}))
 
 
 def time_graph(fn_list, warmup, dev):
@@ -163,7 +196,7 @@ def setup_cfg1(args, dev):
 
     return wl, [mk(i) for i in range(args.steps)], {
         "bytes": synth.algorithmic_bytes(1), "flops": synth.algorithmic_flops(1), "bound": "hbm",
-        "kernel": "qmv_kernel<4,16,1>", "sets": len(sets),
+        "kernel": "qmv64_kernel<1,1>", "sets": len(sets),
         "workload": "decode gate_up gather_qmm + SwiGLU: 1 token, H=2048, E=256, top_k=10, "
                     "W [256,1024,2048] int4 g64 bf16 scale/bias -> h [10,512]"}
 
@@ -187,7 +220,7 @@ def setup_cfg0(args, dev):
 
     return wl, [mk(i) for i in range(args.steps)], {
         "bytes": synth.algorithmic_bytes(0), "flops": synth.algorithmic_flops(0), "bound": "hbm",
-        "kernel": "qmv_kernel<4,16,0>", "sets": len(sets),
+        "kernel": "qmv64_kernel<1,0>", "sets": len(sets),
         "workload": "dense quantized_matmul x [1,2048] . W [4096,2048] int4 g64"}
 
 
@@ -366,6 +399,9 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     cfgs = [int(c) for c in args.configs.split(",") if c != ""]
+    if args.only == "copy":
+        calibration_copy(dev)
+        return 0
     if args.only is not None:
         cfgs = [int(args.only)]
     results = {}
@@ -374,7 +410,7 @@ def main():
         print(f"[bench] workload {cfg}: setup", file=sys.stderr, flush=True)
         wl, fns, meta = SETUPS[cfg](args, dev)
         print(f"[bench] workload {cfg}: timing {len(fns)} steps", file=sys.stderr, flush=True)
-        sec, _g = time_graph(fns, args.warmup, dev)
+        sec, _g = (time_eager if args.eager else time_graph)(fns, args.warmup, dev)
         res = {"workload": meta["workload"], "us_per_call": round(sec * 1e6, 3), "kernel": meta["kernel"],
                "weight_sets": meta["sets"]}
         if meta["bound"] == "hbm":

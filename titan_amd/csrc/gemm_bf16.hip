@@ -4,31 +4,63 @@
 // bf16 as bf16_rne(fmaf(q, s, b)) (:343-344), bf16 x bf16 products, fp32
 // accumulation.  Work unit: one (tile, column block).  A tile is up to
 // kBM = 128 consecutive sorted rows of one expert (the tile list of the
-// routing step); a column block is kBN = 256 output columns, one 64-column
-// slice per wave.
+// routing step); a column block is 64 * W output columns, one 64-column
+// slice for each of the block's W waves (W = 8 when N is a multiple of 512,
+// else 4).  Wide column blocks matter: the activation rows of a tile are
+// fetched once per column block, and that re-fetch, not arithmetic, is the
+// limit at 256 columns.
 //
-// Data flow per 64-wide K group (one quantisation group):
-//   A  the tile's activation rows (gathered through x_rows) are staged in LDS,
-//      double-buffered, shared by the four waves;
-//   B  each lane loads the 16 packed bytes of its own column and half-group,
-//      dequantises them in registers straight into the MFMA B operand -- the
-//      columns of a wave are its own, so B never touches LDS;
-//   four k-steps of v_mfma_f32_32x32x16_bf16 per (32-row, 32-column) subtile.
-// Row subtiles past the tile's valid rows are skipped, so a short tail tile
-// costs only the MFMAs of its 32-row subtiles.
+// Data movement: every operand byte reaches LDS through asynchronous copies
+// (global_load_lds_dwordx4 / _dword, issued from inline assembly so that the
+// copies stay in flight across iterations; the wait counts are explicit).  A
+// ring of kStages stages each holds one 64-wide K group (one quantisation
+// group):
+//   A  the tile's activation rows, gathered through x_rows, 128 x 128 bytes,
+//      16-byte units XOR-swizzled by row (swz) so MFMA operand reads are
+//      bank-conflict free;
+//   B  each wave's 64 columns of packed codes (16 bytes per lane and column
+//      subtile: the lane's own half group);
+//   S  the 64 columns' scales and biases.
+// Per group a wave dequantises its own codes in registers into the MFMA B
+// operand (columns are wave-private, so no dequant work is repeated) and runs
+// four k-steps of v_mfma_f32_32x32x16_bf16 per 32 x 32 subtile.  Row subtiles
+// past the tile's valid rows are compiled out (the loop is instantiated per
+// subtile count), so a short tail tile costs only its own MFMAs.
 //
-// K-order inside a group is free as long as A and B agree: lane half h
-// (lanes 32h..32h+31) supplies group elements 32h + 8*kk .. +7 at k-step kk,
-// which is word kk of the lane's 16-byte code load and bytes 64h + 16kk of the
-// row's 128-byte group segment.
+// K order inside a group is free as long as A and B agree: lane half h
+// supplies group elements 32h + 8kk .. +7 at k-step kk -- word kk of the
+// lane's 16-byte code chunk and 16-byte unit 4h + kk of the activation row.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
 
 constexpr int kBM = 128;
-constexpr int kBN = 256;
-constexpr int kThreads = 256;
-constexpr int kLDA = 72;  // bf16 per LDS row: 64 + 8 pad keeps b128 reads conflict-free
+constexpr int kABytes = kBM * 128;  // one group of the tile's activation rows: 16 KiB
+
+// Layout and pipeline of one instantiation with W waves per block.  W = 8:
+// 512 columns, a ring of 4 stages of 36 KiB, one block per CU.  W = 4: 256
+// columns, 2 stages of 26 KiB, two blocks per CU.
+template <int W>
+struct Cfg {
+  static constexpr int kWaves = W;
+  static constexpr int kBN = 64 * W;
+  static constexpr int kThreads = 64 * W;
+  static constexpr int kStages = W == 8 ? 4 : 2;
+  static constexpr int kBlocksPerCU = W == 8 ? 1 : 2;
+  // stage layout (bytes)
+  static constexpr int kAOff = 0;
+  static constexpr int kBOff = kAOff + kABytes;
+  static constexpr int kBBytes = W * 2 * 64 * 16;  // [wave][subtile][lane] x 16 B
+  static constexpr int kSOff = kBOff + kBBytes;
+  static constexpr int kSBytes = W * 2 * 64 * 4;  // [wave][scale|bias][lane] x 4 B
+  static constexpr int kStageBytes = kSOff + kSBytes;
+  static constexpr int kACopies = kABytes / (W * 1024);  // 16-byte-per-lane copies of A per wave
+  static constexpr int kDmaPerGroup = kACopies + 4;      // + 2 B + 2 S
+  static_assert(kStages * kStageBytes * kBlocksPerCU <= 160 * 1024, "LDS per CU");
+  static_assert(kStages >= 2 && kStages <= 4, "wait_group covers up to two groups in flight");
+};
 
 struct GemmArgs {
   const uint16_t* x;
@@ -47,10 +79,35 @@ struct GemmArgs {
   uint16_t* out;
 };
 
-// bf16 element i (0..7) of a 16-byte chunk
-__device__ __forceinline__ float bf16_at(const uint4& c, int i) {
-  const uint32_t w = (i & 4) ? ((i & 2) ? c.w : c.z) : ((i & 2) ? c.y : c.x);
-  return (i & 1) ? bf16hi(w) : bf16lo(w);
+// Asynchronous 16- and 4-byte copies into LDS: lane i writes
+// lds_base + i * size.  M0 carries the wave's LDS base and is restored.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_base), "v"(g)
+      : "memory");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_base), "v"(g)
+      : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
@@ -60,37 +117,131 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// Byte b of v as a float: one v_cvt_f32_ubyte<b>.  Written as assembly
+// because the compiler otherwise folds the preceding nibble mask into a
+// bit-field extract and spends two instructions per code.
+template <int B>
+__device__ __forceinline__ float ubyte(uint32_t v) {
+  float r;
+  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
 // 8 codes of one word -> 8 bf16 (k order 0..7), bf16_rne(fmaf(q, s, b)).
+// lo holds codes 0,2,4,6 in its bytes, hi codes 1,3,5,7.
 __device__ __forceinline__ i32x4_t dequant_word(uint32_t v, float s, float b) {
   const uint32_t lo = v & 0x0F0F0F0Fu;
   const uint32_t hi = (v >> 4) & 0x0F0F0F0Fu;
   i32x4_t r;
-  r[0] = (int)cvt_pk_bf16(__builtin_fmaf((float)(lo & 0xFFu), s, b), __builtin_fmaf((float)(hi & 0xFFu), s, b));
-  r[1] = (int)cvt_pk_bf16(__builtin_fmaf((float)((lo >> 8) & 0xFFu), s, b),
-                          __builtin_fmaf((float)((hi >> 8) & 0xFFu), s, b));
-  r[2] = (int)cvt_pk_bf16(__builtin_fmaf((float)((lo >> 16) & 0xFFu), s, b),
-                          __builtin_fmaf((float)((hi >> 16) & 0xFFu), s, b));
-  r[3] = (int)cvt_pk_bf16(__builtin_fmaf((float)(lo >> 24), s, b), __builtin_fmaf((float)(hi >> 24), s, b));
+  r[0] = (int)cvt_pk_bf16(__builtin_fmaf(ubyte<0>(lo), s, b), __builtin_fmaf(ubyte<0>(hi), s, b));
+  r[1] = (int)cvt_pk_bf16(__builtin_fmaf(ubyte<1>(lo), s, b), __builtin_fmaf(ubyte<1>(hi), s, b));
+  r[2] = (int)cvt_pk_bf16(__builtin_fmaf(ubyte<2>(lo), s, b), __builtin_fmaf(ubyte<2>(hi), s, b));
+  r[3] = (int)cvt_pk_bf16(__builtin_fmaf(ubyte<3>(lo), s, b), __builtin_fmaf(ubyte<3>(hi), s, b));
   return r;
 }
 
-struct BFrag {
-  i32x4_t v[2][4];  // [column subtile][k-step]
+// Row swizzle of the 16-byte units of an activation row in LDS: unit u of
+// row r is stored at u ^ swz(r).  Conflict-free for b128 reads of one unit by
+// consecutive rows whether the LDS serves 8 lanes per pass over 32 banks
+// (swz distinct over rows r..r+7) or 16 lanes over 64 banks (swz distinct
+// over the eight rows of each parity among r..r+15).
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+template <int W>
+struct Ctx {
+  // per-lane global sources at group 0 (advance per group)
+  const char* a_src[Cfg<W>::kACopies];  // activation 16-byte units, one per A copy
+  const char* b_src[2];  // packed codes of the lane's column in each subtile
+  const char* s_src;     // scale pair (groups 2j, 2j+1) of column (wave*64 + lane)
+  const char* z_src;     // bias pair
+  uint32_t lds;          // LDS address of the ring
+  uint32_t a_dst[Cfg<W>::kACopies];  // wave-uniform LDS offsets within a stage
+  uint32_t b_dst[2];
+  uint32_t s_dst, z_dst;
+  int G;
+  int wave, lane, l32, h;
 };
 
-__device__ __forceinline__ void dequant_b(const uint4 (&raw)[2], const float (&s)[2], const float (&b)[2],
-                                          BFrag& f) {
+template <int W>
+__device__ __forceinline__ void issue_group(const Ctx<W>& c, int g) {
+  using C = Cfg<W>;
+  const uint32_t st = c.lds + (uint32_t)(g % C::kStages) * C::kStageBytes;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    f.v[j][0] = dequant_word(raw[j].x, s[j], b[j]);
-    f.v[j][1] = dequant_word(raw[j].y, s[j], b[j]);
-    f.v[j][2] = dequant_word(raw[j].z, s[j], b[j]);
-    f.v[j][3] = dequant_word(raw[j].w, s[j], b[j]);
+  for (int q = 0; q < C::kACopies; ++q) dma16(c.a_src[q] + (size_t)g * 128, st + c.a_dst[q]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) dma16(c.b_src[j] + (size_t)g * 32, st + c.b_dst[j]);
+  dma4(c.s_src + (size_t)(g >> 1) * 4, st + c.s_dst);
+  dma4(c.z_src + (size_t)(g >> 1) * 4, st + c.z_dst);
+}
+
+// Wait until this wave's copies of group g have landed: the copies of the
+// groups issued after it (at most kStages - 2, each kDmaPerGroup copies)
+// may stay in flight.
+template <int W>
+__device__ __forceinline__ void wait_group(int ahead) {
+  constexpr int D = Cfg<W>::kDmaPerGroup;
+  if (ahead >= 2) wait_vmem<2 * D>();
+  else if (ahead == 1) wait_vmem<D>();
+  else wait_vmem<0>();
+}
+
+template <int W, int MSUB>
+__device__ __forceinline__ void tile_loop(const Ctx<W>& c, const char* smem, f32x16_t (&acc)[4][2]) {
+  using C = Cfg<W>;
+  constexpr int kStages = C::kStages, kAOff = C::kAOff, kBOff = C::kBOff, kSOff = C::kSOff;
+  const int G = c.G;
+#pragma unroll
+  for (int d = 0; d < kStages - 1; ++d)
+    if (d < G) issue_group(c, d);
+
+  for (int g = 0; g < G; ++g) {
+    wait_group<W>(min(kStages - 2, G - 1 - g));
+    __builtin_amdgcn_s_barrier();
+    if (g + kStages - 1 < G) issue_group(c, g + kStages - 1);
+
+    const char* st = smem + (g % kStages) * C::kStageBytes;
+    // this lane's codes, scales and biases for its two columns
+    const uint4 raw0 = *reinterpret_cast<const uint4*>(st + kBOff + (c.wave * 2 + 0) * 1024 + c.lane * 16);
+    const uint4 raw1 = *reinterpret_cast<const uint4*>(st + kBOff + (c.wave * 2 + 1) * 1024 + c.lane * 16);
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + kSOff + c.wave * 512);
+    const int sh = (g & 1) ? 16 : 0;
+    const float s0 = __uint_as_float((sw[c.l32] >> sh) << 16);
+    const float s1 = __uint_as_float((sw[c.l32 + 32] >> sh) << 16);
+    const float z0 = __uint_as_float((sw[64 + c.l32] >> sh) << 16);
+    const float z1 = __uint_as_float((sw[64 + c.l32 + 32] >> sh) << 16);
+    const uint32_t w0[4] = {raw0.x, raw0.y, raw0.z, raw0.w};
+    const uint32_t w1[4] = {raw1.x, raw1.y, raw1.z, raw1.w};
+    const char* abuf = st + kAOff;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const i32x4_t b0 = dequant_word(w0[kk], s0, z0);
+      const i32x4_t b1 = dequant_word(w1[kk], s1, z1);
+      i32x4_t af[MSUB];
+#pragma unroll
+      for (int i = 0; i < MSUB; ++i) {
+        const int row = 32 * i + c.l32;  // swz(row) == swz(l32): 32*i leaves bits 0..3 alone
+        const int unit = (4 * c.h + kk) ^ swz(c.l32);
+        af[i] = *reinterpret_cast<const i32x4_t*>(abuf + row * 128 + unit * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < MSUB; ++i) {
+        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, af[i]),
+                                                            __builtin_bit_cast(bf16x8_t, b0), acc[i][0], 0, 0, 0);
+        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, af[i]),
+                                                            __builtin_bit_cast(bf16x8_t, b1), acc[i][1], 0, 0, 0);
+      }
+    }
   }
 }
 
-__global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM * kLDA];
+template <int W>
+__global__ __launch_bounds__(Cfg<W>::kThreads, Cfg<W>::kBlocksPerCU) void gemm_bf16_kernel(GemmArgs a) {
+  using C = Cfg<W>;
+  constexpr int kBN = C::kBN, kWaves = C::kWaves;
+  __shared__ __attribute__((aligned(1024))) char smem[C::kStages * C::kStageBytes];
 
   const int NB = a.N / kBN;
   const int64_t n_active = (int64_t)a.ntiles[0] * NB;
@@ -115,30 +266,36 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmArgs a) {
   const int G = K / 64;
   const int64_t KW = K / 8;
   const int tid = threadIdx.x;
-  const int wave = tid / 64;
-  const int lane = tid % 64;
-  const int l32 = lane % 32;
-  const int h = lane / 32;
 
-  // A staging: thread -> (row, half of the 128-byte group segment)
-  const int arow = tid >> 1;
-  const int ahalf = tid & 1;
-  int64_t src = row0 + min(arow, valid - 1);
-  if (a.x_rows) src = a.x_rows[src];
-  const uint4* aptr = reinterpret_cast<const uint4*>(a.x + src * K + ahalf * 32);
-  uint16_t* const adst0 = &As[0][arow * kLDA + ahalf * 32];
-  uint16_t* const adst1 = &As[1][arow * kLDA + ahalf * 32];
-
-  // B: this lane's two columns
-  const int ncol = nblk * kBN + wave * 64 + l32;
-  const int64_t c0 = (int64_t)e * a.N + ncol;
-  const int64_t c1 = c0 + 32;
-  const uint4* bp0 = reinterpret_cast<const uint4*>(a.w + c0 * KW) + h;
-  const uint4* bp1 = reinterpret_cast<const uint4*>(a.w + c1 * KW) + h;
-  const uint4* sp0 = reinterpret_cast<const uint4*>(a.s + c0 * G);
-  const uint4* sp1 = reinterpret_cast<const uint4*>(a.s + c1 * G);
-  const uint4* zp0 = reinterpret_cast<const uint4*>(a.b + c0 * G);
-  const uint4* zp1 = reinterpret_cast<const uint4*>(a.b + c1 * G);
+  Ctx<W> c;
+  c.G = G;
+  c.wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  c.lane = tid % 64;
+  c.l32 = c.lane % 32;
+  c.h = c.lane / 32;
+  c.lds = (uint32_t)(uintptr_t)smem;
+  // A copies: wave w, copy q writes stage units (q*kWaves + w)*64 + lane, i.e.
+  // row p/8 and stored unit p%8, which holds logical unit (p%8) ^ swz(row).
+#pragma unroll
+  for (int q = 0; q < C::kACopies; ++q) {
+    const int p = (q * kWaves + c.wave) * 64 + c.lane;
+    const int row = p >> 3;
+    const int unit = (p & 7) ^ swz(row);
+    int64_t src = row0 + min(row, valid - 1);
+    if (a.x_rows) src = a.x_rows[src];
+    c.a_src[q] = reinterpret_cast<const char*>(a.x + src * K + unit * 8);
+    c.a_dst[q] = (uint32_t)(C::kAOff + (q * kWaves + c.wave) * 1024);
+  }
+  const int64_t col_base = (int64_t)e * a.N + nblk * kBN + c.wave * 64;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    c.b_src[j] = reinterpret_cast<const char*>(a.w + (col_base + j * 32 + c.l32) * KW + c.h * 4);
+    c.b_dst[j] = (uint32_t)(C::kBOff + (c.wave * 2 + j) * 1024);
+  }
+  c.s_src = reinterpret_cast<const char*>(a.s + (col_base + c.lane) * G);
+  c.z_src = reinterpret_cast<const char*>(a.b + (col_base + c.lane) * G);
+  c.s_dst = (uint32_t)(C::kSOff + c.wave * 512);
+  c.z_dst = c.s_dst + 256;
 
   f32x16_t acc[4][2];
 #pragma unroll
@@ -148,84 +305,22 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  uint4 areg[4];
-  uint4 braw[2];
-  uint4 sch[2], bch[2];  // 8 groups of scales / biases per column
-  BFrag fa, fb;
-
-  // prologue: group 0
-#pragma unroll
-  for (int c = 0; c < 4; ++c) areg[c] = aptr[c];
-  braw[0] = bp0[0];
-  braw[1] = bp1[0];
-  sch[0] = sp0[0];
-  sch[1] = sp1[0];
-  bch[0] = zp0[0];
-  bch[1] = zp1[0];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) reinterpret_cast<uint4*>(adst0)[c] = areg[c];
-  {
-    const float s2[2] = {bf16_at(sch[0], 0), bf16_at(sch[1], 0)};
-    const float b2[2] = {bf16_at(bch[0], 0), bf16_at(bch[1], 0)};
-    dequant_b(braw, s2, b2, fa);
-  }
-
-  auto step = [&](int g, const BFrag& cur, BFrag& nxt) {
-    const bool more = g + 1 < G;
-    if (more) {
-      const int gn = g + 1;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) areg[c] = aptr[gn * 8 + c];
-      braw[0] = bp0[gn * 2];
-      braw[1] = bp1[gn * 2];
-      if ((gn & 7) == 0) {
-        sch[0] = sp0[gn >> 3];
-        sch[1] = sp1[gn >> 3];
-        bch[0] = zp0[gn >> 3];
-        bch[1] = zp1[gn >> 3];
-      }
-    }
-    __syncthreads();
-    const uint16_t* abuf = As[g & 1];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (i < msub) {
-          const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf + (32 * i + l32) * kLDA + 32 * h + 8 * kk);
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, af),
-                                                                __builtin_bit_cast(bf16x8_t, cur.v[j][kk]),
-                                                                acc[i][j], 0, 0, 0);
-          }
-        }
-      }
-    }
-    if (more) {
-      uint16_t* d = (g & 1) ? adst0 : adst1;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) reinterpret_cast<uint4*>(d)[c] = areg[c];
-      const int gi = (g + 1) & 7;
-      const float s2[2] = {bf16_at(sch[0], gi), bf16_at(sch[1], gi)};
-      const float b2[2] = {bf16_at(bch[0], gi), bf16_at(bch[1], gi)};
-      dequant_b(braw, s2, b2, nxt);
-    }
-  };
-
-  for (int g = 0; g < G; g += 2) {
-    step(g, fa, fb);
-    step(g + 1, fb, fa);
+  switch (msub) {
+    case 1: tile_loop<W, 1>(c, smem, acc); break;
+    case 2: tile_loop<W, 2>(c, smem, acc); break;
+    case 3: tile_loop<W, 3>(c, smem, acc); break;
+    default: tile_loop<W, 4>(c, smem, acc); break;
   }
 
   // epilogue: D[m][n] of a 32x32 subtile sits in lane n (mod 32), register
   // r at row 8*(r/4) + 4*(lane/32) + r%4.
+  const int ncol = nblk * kBN + c.wave * 64 + c.l32;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (i >= msub) continue;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
+      const int m = 32 * i + 8 * (r / 4) + 4 * c.h + (r % 4);
       if (m < valid) {
         uint16_t* orow = a.out + (row0 + m) * (int64_t)a.N + ncol;
         orow[0] = (uint16_t)f32_to_bf16(acc[i][0][r]);
@@ -254,15 +349,20 @@ extern "C" int qmoe_gather_qmm_sorted(const uint16_t* x, const int32_t* x_rows, 
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sorted GEMM takes 4-bit codes with group_size 64 (got %d, %d)",
                       bits, group_size);
   if (K % 1024) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 1024", (long long)K);
-  if (N % kBN) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of %d", (long long)N, kBN);
+  if (N % 256) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of 256", (long long)N);
   if (!qmoe::aligned16(x) || !qmoe::aligned16(w) || !qmoe::aligned16(scales) || !qmoe::aligned16(biases))
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x, w, scales and biases must be 16-byte aligned");
   if (K > 0x7FFFFFFF || N > 0x7FFFFFFF || n_rows > 0x7FFFFFFF)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
-  const int64_t blocks = max_tiles * (N / kBN);
+  const bool wide = N % Cfg<8>::kBN == 0;
+  const int64_t blocks = max_tiles * (N / (wide ? Cfg<8>::kBN : Cfg<4>::kBN));
   if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
   GemmArgs a{x, x_rows, n_rows, (int)K, w, scales, biases, num_experts, (int)N, offsets, tile_row, tile_exp, ntiles,
              out};
-  gemm_bf16_kernel<<<dim3((unsigned)blocks), dim3(kThreads), 0, qmoe::as_stream(stream)>>>(a);
+  hipStream_t st = qmoe::as_stream(stream);
+  if (wide)
+    gemm_bf16_kernel<8><<<dim3((unsigned)blocks), dim3(Cfg<8>::kThreads), 0, st>>>(a);
+  else
+    gemm_bf16_kernel<4><<<dim3((unsigned)blocks), dim3(Cfg<4>::kThreads), 0, st>>>(a);
   return qmoe::launch_status("gemm_bf16_kernel");
 }

@@ -146,6 +146,111 @@ __global__ __launch_bounds__(64) void qmv_kernel(QmvArgs a) {
   }
 }
 
+// ---- whole-wave rows: the K = 2048 * NV fast path ------------------------
+//
+// A wave reduces eight weight rows at once; lane l owns chunks
+// k = v*2048 + l*32 .. +31 of every row (NV chunks), so one 16-byte load per
+// lane and chunk covers 1 KiB of a row.  The eight per-lane partials are
+// reduced together: two lane-swap folds (v_permlane32_swap,
+// v_permlane16_swap), a row_ror:8 fold and three DPP adds leave row q's sum
+// in lanes 8q..8q+7 -- 19 operations for eight rows instead of a
+// six-step shuffle tree per row.  Weight loads are non-temporal: every byte
+// is used once.
+
+__device__ __forceinline__ float as_f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t as_u(float f) { return __float_as_uint(f); }
+// lanes < 32: a(l) + a(l+32); lanes >= 32: b(l-32) + b(l)
+__device__ __forceinline__ float fold32(float a, float b) {
+  auto r = __builtin_amdgcn_permlane32_swap(as_u(a), as_u(b), false, false);
+  return as_f(r[0]) + as_f(r[1]);
+}
+// per 32-lane half: lanes [0,16): a(l) + a(l+16); [16,32): b(l-16) + b(l)
+__device__ __forceinline__ float fold16(float a, float b) {
+  auto r = __builtin_amdgcn_permlane16_swap(as_u(a), as_u(b), false, false);
+  return as_f(r[0]) + as_f(r[1]);
+}
+// per 16-lane row: lanes [0,8): a(l) + a(l+8); [8,16): b(l-8) + b(l)
+__device__ __forceinline__ float fold8(float a, float b, int lane) {
+  const bool hi = lane & 8;
+  const float send = hi ? a : b, keep = hi ? b : a;
+  return keep + as_f(__builtin_amdgcn_update_dpp(0, as_u(send), 0x128, 0xf, 0xf, false));  // row_ror:8
+}
+__device__ __forceinline__ float sum8(float v) {
+  v += as_f(__builtin_amdgcn_update_dpp(0, as_u(v), 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  v += as_f(__builtin_amdgcn_update_dpp(0, as_u(v), 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  v += as_f(__builtin_amdgcn_update_dpp(0, as_u(v), 0x141, 0xf, 0xf, false));  // row_half_mirror
+  return v;
+}
+// eight per-lane partials -> 64-lane sums; lanes 8q..8q+7 hold sum q
+__device__ __forceinline__ float reduce8(const float (&v)[8], int lane) {
+  const float r0 = fold32(v[0], v[4]), r1 = fold32(v[1], v[5]), r2 = fold32(v[2], v[6]),
+              r3 = fold32(v[3], v[7]);
+  return sum8(fold8(fold16(r0, r2), fold16(r1, r3), lane));
+}
+
+__device__ __forceinline__ uint4 load_nt(const uint4* p) {
+  const i32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));
+  return make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
+}
+
+// MODE 0: eight outputs per wave; MODE 1: four gate/up pairs per wave.
+template <int NV, int MODE>
+__global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
+  constexpr int OUTS = MODE == 1 ? 4 : 8;
+  const int lane = threadIdx.x;
+  const int64_t nblk = (a.n_out + OUTS - 1) / OUTS;
+  const int64_t r = blockIdx.x / nblk;
+  if (r >= a.n_pairs) return;
+  const int n0 = (int)(blockIdx.x % nblk) * OUTS;
+  int e = a.experts ? a.experts[r] : 0;
+  e = min(max(e, 0), a.num_experts - 1);
+  const int64_t xr = a.x_rows ? (int64_t)a.x_rows[r] : r / a.x_div;
+  const int K = a.K;
+  const int G = K / a.group_size;
+  const int64_t KW = K / 8;
+  const int64_t ebase = (int64_t)e * a.n_w;
+
+  uint4 wv[8][NV];
+  float sv[8][NV], bv[8][NV];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int oq = MODE == 1 ? (q & 3) : q;
+    const int n = min(n0 + oq, a.n_out - 1);
+    const int64_t row = ebase + n + ((MODE == 1 && q >= 4) ? a.n_out : 0);
+    const uint4* p = reinterpret_cast<const uint4*>(a.w + row * KW) + lane;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      wv[q][v] = load_nt(p + v * 64);
+      const int g = (v * 2048 + lane * 32) / a.group_size;
+      sv[q][v] = bf16_to_f32(a.s[row * G + g]);
+      bv[q][v] = bf16_to_f32(a.b[row * G + g]);
+    }
+  }
+  const uint16_t* xrow = a.x + xr * a.x_stride;
+  XChunk xc[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) load_x_chunk(xrow + v * 2048 + lane * 32, xc[v]);
+  float part[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    part[q] = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) part[q] += affine_chunk(dot_chunk(wv[q][v], xc[v]), xc[v].sum, sv[q][v], bv[q][v]);
+  }
+  const float t = reduce8(part, lane);  // lanes 8q..: row q
+  if (MODE == 1) {
+    // gate q sits in lanes 8q (q < 4), up q in lanes 8q + 32
+    auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
+    const float up = as_f(sw[1]);
+    const int q = lane >> 3;
+    if (lane < 32 && (lane & 7) == 0 && n0 + q < a.n_out)
+      a.out[r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t / (1.0f + expf(-t)) * up);
+  } else {
+    const int q = lane >> 3;
+    if ((lane & 7) == 0 && n0 + q < a.n_out) a.out[r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t);
+  }
+}
+
 struct DownArgs {
   const uint16_t* h;  // [T, k, I]
   const int32_t* idx; // [T, k]
@@ -234,6 +339,20 @@ bool pick_split(int64_t K, int* lpr, int* nv) {
 
 template <int MODE>
 int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st) {
+  if (a.K % 2048 == 0 && a.K / 2048 <= 4) {
+    constexpr int outs = MODE == 1 ? 4 : 8;
+    const int64_t blocks = a.n_pairs * ((a.n_out + outs - 1) / outs);
+    if (blocks <= 0) return QMOE_OK;
+    if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
+    dim3 grid((unsigned)blocks), block(64);
+    switch (a.K / 2048) {
+      case 1: qmv64_kernel<1, MODE><<<grid, block, 0, st>>>(a); break;
+      case 2: qmv64_kernel<2, MODE><<<grid, block, 0, st>>>(a); break;
+      case 3: qmv64_kernel<3, MODE><<<grid, block, 0, st>>>(a); break;
+      default: qmv64_kernel<4, MODE><<<grid, block, 0, st>>>(a); break;
+    }
+    return qmoe::launch_status("qmv64_kernel");
+  }
   const int gpw = 64 / lpr;
   const int64_t nblk = (a.n_out + gpw - 1) / gpw;
   const int64_t blocks = a.n_pairs * nblk;

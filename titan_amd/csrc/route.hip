@@ -4,7 +4,7 @@
 // Replaces _gather_sort (switch_layers.py:13-18: two mx.argsort calls and a
 // gather) and the single-threadgroup tile walk of build_tiles
 // (titan/kernels/moe_gather_ws.py:133-156) with three launches:
-//   count   one block per CHUNK rows: per-chunk expert histogram in LDS
+//   count   one block per 1024-row chunk: per-chunk expert histogram in LDS
 //   scan    one block: expert-major exclusive scan of the histograms, which
 //           gives each (expert, chunk) its first output slot, the offsets,
 //           and the tile list
@@ -16,21 +16,26 @@
 
 namespace {
 
-constexpr int kChunk = 256;
+constexpr int kChunk = 1024;    // rows per histogram chunk
+constexpr int kCountThreads = 256;
 constexpr int kScanThreads = 1024;
 
 __device__ __forceinline__ int clamp_id(int id, int E) { return id < 0 ? 0 : (id >= E ? E - 1 : id); }
 
-__global__ __launch_bounds__(256) void route_count_kernel(const int32_t* __restrict__ ids, int64_t n,
-                                                          int E, int nchunks, int32_t* __restrict__ counts) {
+__global__ __launch_bounds__(kCountThreads) void route_count_kernel(const int32_t* __restrict__ ids, int64_t n,
+                                                                    int E, int nchunks,
+                                                                    int32_t* __restrict__ counts) {
   extern __shared__ int hist[];  // E + 1 (last slot: out-of-range ids)
   for (int e = threadIdx.x; e <= E; e += blockDim.x) hist[e] = 0;
   __syncthreads();
-  const int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
-  if (i < n) {
-    const int id = ids[i];
-    if (id < 0 || id >= E) atomicAdd(&hist[E], 1);
-    atomicAdd(&hist[clamp_id(id, E)], 1);
+#pragma unroll
+  for (int q = 0; q < kChunk / kCountThreads; ++q) {
+    const int64_t i = (int64_t)blockIdx.x * kChunk + q * kCountThreads + threadIdx.x;
+    if (i < n) {
+      const int id = ids[i];
+      if (id < 0 || id >= E) atomicAdd(&hist[E], 1);
+      atomicAdd(&hist[clamp_id(id, E)], 1);
+    }
   }
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += blockDim.x) counts[(int64_t)e * nchunks + blockIdx.x] = hist[e];
@@ -53,19 +58,32 @@ __device__ int block_exclusive_scan(int v, int* lds, int* total) {
   return incl - v;
 }
 
-// Exclusive scan, in place, of a[0..L) with one block.
+// Exclusive scan, in place, of a[0..L) with one block.  Each thread owns a
+// contiguous segment, read in batches of 16 independent loads so the reads
+// overlap instead of paying one memory latency per element.
 __device__ int block_scan_array(int32_t* a, int64_t L, int* lds) {
   const int tid = threadIdx.x;
   const int64_t seg = (L + kScanThreads - 1) / kScanThreads;
   const int64_t lo = min((int64_t)tid * seg, L), hi = min(lo + seg, L);
   int local = 0;
-  for (int64_t i = lo; i < hi; ++i) local += a[i];
+  for (int64_t b = lo; b < hi; b += 16) {
+    int v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (b + i < hi) ? a[b + i] : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) local += v[i];
+  }
   int total;
   int run = block_exclusive_scan(local, lds, &total);
-  for (int64_t i = lo; i < hi; ++i) {
-    const int c = a[i];
-    a[i] = run;
-    run += c;
+  for (int64_t b = lo; b < hi; b += 16) {
+    int v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (b + i < hi) ? a[b + i] : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (b + i < hi) a[b + i] = run;
+      run += v[i];
+    }
   }
   __syncthreads();
   return total;
@@ -132,10 +150,18 @@ __global__ __launch_bounds__(64) void route_scatter_kernel(const int32_t* __rest
   for (int e = lane; e < E; e += 64) run[e] = base[(int64_t)e * nchunks + c];
   __syncthreads();
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int step = 0; step < kChunk / 64; ++step) {
+  constexpr int kSteps = kChunk / 64;
+  int idv[kSteps];  // the chunk's ids, loaded up front (independent loads)
+#pragma unroll
+  for (int step = 0; step < kSteps; ++step) {
+    const int64_t i = (int64_t)c * kChunk + step * 64 + lane;
+    idv[step] = i < n ? clamp_id(ids[i], E) : E;  // E: sentinel, never written
+  }
+#pragma unroll
+  for (int step = 0; step < kSteps; ++step) {
     const int64_t i = (int64_t)c * kChunk + step * 64 + lane;
     const bool valid = i < n;
-    const int id = valid ? clamp_id(ids[i], E) : E;  // E: sentinel, never written
+    const int id = idv[step];
     uint64_t m = __ballot(valid);
     if (!valid) m = ~m;
     for (int b = 0; b < nbits; ++b) {
@@ -207,7 +233,7 @@ extern "C" int qmoe_route(const int32_t* ids, int64_t n_pairs, int32_t num_exper
   int32_t* bad = ws;
   int32_t* counts = ws + 64;
   if (nch > 0) {
-    route_count_kernel<<<dim3((unsigned)nch), dim3(kChunk), (num_experts + 1) * sizeof(int), st>>>(
+    route_count_kernel<<<dim3((unsigned)nch), dim3(kCountThreads), (num_experts + 1) * sizeof(int), st>>>(
         ids, n_pairs, num_experts, (int)nch, counts);
     int rc = qmoe::launch_status("route_count_kernel");
     if (rc) return rc;
