@@ -30,6 +30,7 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+METRIC = "MoE gather_qmm HBM GB/s (decode), TFLOP/s (prefill), % roofline, 1 MI355X"
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, vendor spec
 BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA, vendor spec
 INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, vendor spec
@@ -390,8 +391,8 @@ def _cpu_model():
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the expert-parallel "
-                                   "sharding is design-only, see DESIGN.md)"}))
+        print(json.dumps({"error": "this path runs on one GPU; --gpus must be 1 (expert-parallel "
+                                   "sharding over several GPUs is not built)"}))
         return 2
     import torch
     from titan_amd import _lib
@@ -443,10 +444,10 @@ def main():
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(1, wl, args.cpu_seconds)
     line = {
-        "metric": "MoE gather_qmm HBM GB/s (decode gate_up, 1 token, top-10)",
+        "metric": METRIC,
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(sec * 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int4 weights (bf16 scale/bias), bf16 activations, fp32 accumulate", "data": "synthetic",
+        "dtype": "bf16", "data": "synthetic",
         "config": {"workload": meta["workload"], "tokens": 1, "top_k": 10, "experts": 256, "hidden": 2048,
                    "intermediate": 512, "group_size": 64, "bits": 4, "weight_sets_rotated": meta["sets"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

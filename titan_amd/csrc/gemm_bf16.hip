@@ -348,7 +348,8 @@ extern "C" int qmoe_gather_qmm_sorted(const uint16_t* x, const int32_t* x_rows, 
   if (bits != 4 || group_size != 64)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sorted GEMM takes 4-bit codes with group_size 64 (got %d, %d)",
                       bits, group_size);
-  if (K % 1024) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 1024", (long long)K);
+  // scales and biases are copied in pairs of groups: K / 64 must be even
+  if (K % 128) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 128", (long long)K);
   if (N % 256) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of 256", (long long)N);
   if (!qmoe::aligned16(x) || !qmoe::aligned16(w) || !qmoe::aligned16(scales) || !qmoe::aligned16(biases))
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x, w, scales and biases must be 16-byte aligned");

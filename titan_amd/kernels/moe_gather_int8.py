@@ -1,0 +1,130 @@
+"""int8-activation x int4-weight sorted-gather MoE matmul on int8 MFMA
+(titan/kernels/moe_gather_int8.py).
+
+Activations are quantised per token, symmetrically: ``sx = max|x| / 127``
+(fp32), ``xi = clamp(rint(x / sx), -127, 127)``.  Per 64-wide group the kernel
+forms ``D = sum xi * q`` with ``v_mfma_i32_32x32x32_i8`` (codes 0..15 are
+valid int8 operands as they are, so no re-centring and no nibble-sum table)
+and ``R = sum xi`` exactly, then ``y = sx * sum_g (s * D + b * R)`` in fp32.
+
+Not exact against the unquantised product, by design: this is the one op whose
+fast path changes the numbers, so, as in the reference
+(moe_gather_int8.py:431-442), it is selected only when the caller passes
+prepared :class:`Int8Tables`, and its test bounds the relative RMS error
+against the fake-quant product ``(sx * xi) @ deq(W)^T``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .. import ops, stock
+from .moe_gather_ws import build_tiles
+from .registry import KernelOp, ShapeClass, shape_class
+
+__all__ = ["BITS", "GROUP", "Int8Tables", "OP", "build_tables", "hip", "key", "pick_cfg",
+           "quantize_activations", "reference", "supports"]
+
+GROUP = 64
+BITS = 4
+
+
+@dataclass(frozen=True)
+class Int8Tables:
+    """Caller-owned prepared state for one weight tensor
+    (moe_gather_int8.py:189-248).  The int8 kernel reads the MLX tensors as
+    they are, so the tables hold the validated operands and no copies; their
+    presence is the caller's opt-in to the approximate path."""
+
+    w: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+
+    @property
+    def nbytes(self) -> int:
+        return 0
+
+
+def build_tables(wq, scales, biases) -> Int8Tables:
+    """Validate and wrap one weight tensor's operands (one-time, per tensor)."""
+    if wq.dim() != 3 or scales.shape != biases.shape or scales.dim() != 3:
+        raise ValueError("expected w [E, N, K/8] and scales/biases [E, N, K/64]")
+    if wq.shape[-1] * 8 != scales.shape[-1] * GROUP:
+        raise ValueError("w and scales disagree on K")
+    return Int8Tables(wq, scales, biases)
+
+
+def pick_cfg(N: int):
+    return (ops.tile_rows(), 4) if N % 256 == 0 else None
+
+
+def quantize_activations(x: torch.Tensor):
+    """Per-token symmetric int8 of bf16 rows: (xi int8 [R, K], sx fp32 [R])."""
+    return ops.quantize_act_int8(x)
+
+
+def reference(x, wq, scales, biases, rhs_indices, tables=None, tiles=None, *, group_size=GROUP, bits=BITS):
+    """The stock (unquantised) gather (moe_gather_int8.py:377-390)."""
+    return stock.gather_qmm(x, wq, scales, biases, rhs_indices=rhs_indices, transpose=True,
+                            group_size=group_size, bits=bits, sorted_indices=True)
+
+
+def hip(x, wq, scales, biases, rhs_indices, tables=None, tiles=None, *, group_size=GROUP, bits=BITS):
+    """Quantise the rows, then the int8 grouped GEMM.  Same signature as
+    :func:`reference`; ``tables`` None builds them for this call."""
+    E, N = int(wq.shape[0]), int(scales.shape[1])
+    if pick_cfg(N) is None:
+        raise ops.QmoeUnsupported(ops._lib.ERR_UNSUPPORTED, f"no int8 tiling for N = {N}")
+    if tables is None:
+        tables = build_tables(wq, scales, biases)
+    R, K = int(x.shape[0]), int(x.shape[-1])
+    if tiles is None:
+        tiles = build_tiles(rhs_indices, E)
+    if tiles.tile_rows != ops.tile_rows() or tiles.num_experts != E or tiles.rows != R:
+        raise ValueError("tile table does not match this call")
+    xi, sx = quantize_activations(x.reshape(R, K))
+    y = ops.gather_qmm_int8_sorted(xi, sx, tables.w, tables.scales, tables.biases, tiles, None, group_size, bits)
+    return y.reshape(R, 1, N)
+
+
+def key(x, wq, scales, biases, rhs_indices, tables=None, tiles=None, *, group_size=GROUP,
+        bits=BITS) -> ShapeClass:
+    return shape_class(x, wq, scales, biases, rhs_indices, extra=(group_size, bits, tables is not None))
+
+
+def supports(k: ShapeClass) -> bool:
+    """Opt-in (tables passed), 4-bit group 64, [R, 1, K] bf16 rows, K a
+    multiple of 1024, N of 256 (moe_gather_int8.py:435-450)."""
+    if k.device != "gpu" or len(k.shapes) != 5 or len(k.extra) != 3:
+        return False
+    group_size, bits, has_tables = k.extra
+    if not has_tables or (group_size, bits) != (GROUP, BITS):
+        return False
+    xs, ws, ss, _bs, idx = k.shapes
+    if len(ws) != 3 or len(ss) != 3 or len(idx) != 1 or k.dtypes[0] != torch.bfloat16:
+        return False
+    if len(xs) != 3 or xs[1] != 1 or xs[0] != idx[0] or xs[-1] % 1024 or xs[0] < ops.SORTED_MIN_ROWS:
+        return False
+    return pick_cfg(ss[1]) is not None
+
+
+OP = KernelOp(
+    name="moe_gather_int8",
+    default_off=True,
+    default_off_reason="changes the numbers (per-token int8 activations); opt in by naming it",
+    aliases=("moe_gather_gate_up",),
+    reference_fn=reference,
+    fast_fn=hip,
+    key=key,
+    supports_key=supports,
+    tolerance=0.01,  # relative RMS against the unquantised product
+    shapes=(
+        {"R": 300, "K": 1024, "N": 256, "E": 8, "bits": 4},
+        {"R": 640, "K": 2048, "N": 512, "E": 16, "bits": 4},
+        {"R": 40960, "K": 2048, "N": 1024, "E": 256, "bits": 4},
+    ),
+    exactness="not exact: per-token int8 activations; integer parts exact, fp32 rescale",
+    source="titan/kernels/moe_gather_int8.py",
+)

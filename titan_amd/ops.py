@@ -257,7 +257,7 @@ def gather_qmm_sorted(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bi
 
 
 def gemm_supported(K: int, N: int, group_size: int, bits: int) -> bool:
-    return bits == 4 and group_size == 64 and K % 1024 == 0 and N % 256 == 0
+    return bits == 4 and group_size == 64 and K % 128 == 0 and N % 256 == 0
 
 
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None = None,

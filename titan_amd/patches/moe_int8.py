@@ -1,0 +1,85 @@
+"""Overlay: route sorted routed-expert prefill gathers through the
+int8-activation x int4-weight grouped GEMM (engine/patches/moe-int8/patch.py).
+
+Routed only when ALL of: ``sorted_indices=True``, ``rhs_indices`` present and
+``lhs_indices`` absent, ``transpose=True``, affine 4-bit ``group_size=64``,
+bf16 rows ``[R, 1, K]`` on the GPU, ``K % 1024 == 0``, ``N % 256 == 0`` and
+the token floor.  Everything else falls through to what was installed before.
+
+    TITAN_AMD_MOE_INT8_PREFILL=1        enable (default off: it changes the numbers)
+    TITAN_AMD_MOE_INT8_MIN_TOKENS=512   token floor of the SwitchGLU call
+    TITAN_AMD_MOE_INT8_MIN_ROWS=4096    routed-row floor when the token count is unknown
+
+Memory: none beyond the call's own activations (the int8 kernel reads the
+MLX-layout weights as they are).
+"""
+
+from __future__ import annotations
+
+from ..kernels import moe_gather_int8 as _k
+from ._overlay import Overlay, arg
+
+MARKER = "_titan_amd_moe_int8"
+
+
+def _key_args(x, w, args, kwargs):
+    return (x, w, arg(args, kwargs, 0, "scales"), arg(args, kwargs, 1, "biases"),
+            arg(args, kwargs, 3, "rhs_indices"))
+
+
+def _should_route(ov, x, w, args, kwargs) -> bool:
+    if not ov.enabled() or not kwargs.get("sorted_indices"):
+        return False
+    if arg(args, kwargs, 2, "lhs_indices") is not None or arg(args, kwargs, 7, "mode", "affine") != "affine":
+        return False
+    if not arg(args, kwargs, 4, "transpose", True):
+        return False
+    if x.dim() < 1 or ov.below_floor(int(x.shape[0])):
+        return False
+    return supported(x, w, *[arg(args, kwargs, i, n) for i, n in ((0, "scales"), (1, "biases"))],
+                     arg(args, kwargs, 3, "rhs_indices"), True, arg(args, kwargs, 5, "group_size", 64),
+                     arg(args, kwargs, 6, "bits", 4))
+
+
+def supported(x, w, scales, biases, rhs, transpose, group_size, bits) -> bool:
+    """Would the int8 kernel take this call (shapes only)?"""
+    if rhs is None or scales is None or biases is None or not transpose:
+        return False
+    return _k.supports(_k.key(x, w, scales, biases, rhs, True, group_size=group_size, bits=bits))
+
+
+def _route(x, w, args, kwargs):
+    return _k.hip(x, w, arg(args, kwargs, 0, "scales"), arg(args, kwargs, 1, "biases"),
+                  arg(args, kwargs, 3, "rhs_indices"), group_size=arg(args, kwargs, 5, "group_size", 64),
+                  bits=arg(args, kwargs, 6, "bits", 4))
+
+
+_OV = Overlay("moe int8 prefill", MARKER, "TITAN_AMD_MOE_INT8_PREFILL", False,
+              {"gather_qmm": (_should_route, _route)}, "TITAN_AMD_MOE_INT8_MIN_TOKENS", 512,
+              "TITAN_AMD_MOE_INT8_MIN_ROWS", 4096)
+
+
+def enabled() -> bool:
+    return _OV.enabled()
+
+
+def install(namespace=None) -> bool:
+    """Idempotent.  Returns True when this call installed the hooks."""
+    return _OV.install(namespace)
+
+
+def uninstall() -> None:
+    _OV.uninstall()
+
+
+def stats() -> dict:
+    return _OV.stats()
+
+
+def clear_cache() -> None:
+    """Nothing is cached: the tables are the caller's."""
+
+
+def warmup(model=None) -> int:
+    """Nothing to precompute."""
+    return 0
