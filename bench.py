@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--only", default=None,
                     help="run one workload's timed loop only, or 'copy' for the calibration copy kernel")
     ap.add_argument("--eager", action="store_true", help="launch the timed steps eagerly (no graph)")
+    ap.add_argument("--traffic", action="store_true",
+                    help="measure the decode kernel's HBM traffic live with rocprofv3 counter passes")
     return ap.parse_args()
 
 
@@ -114,10 +116,14 @@ def time_eager(fn_list, warmup, dev):
         fn()
     e1.record(st)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / len(fn_list), None
+    sec = e0.elapsed_time(e1) / 1e3 / len(fn_list)
+    return sec, {"min": sec, "median": sec, "rounds": 1, "graphs": None}
 
 
-def calibration_copy(dev, mib=256, reps=5):
+CALIBRATION_MIB = 256
+
+
+def calibration_copy(dev, mib=CALIBRATION_MIB, reps=5):
     """A plain device copy of known size: the scale for HBM byte counters."""
     import torch
 
@@ -130,33 +136,130 @@ def calibration_copy(dev, mib=256, reps=5):
     print(json.dumps({"calibration_copy_bytes_read": n * 4, "bytes_written": n * 4, "reps": reps}))
 
 
+# ------------------------------------------------------------- HBM traffic
+#
+# rocprofv3 FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel,
+# scaled by what the same counters read for a plain device copy of known size.
+# `--traffic` measures them live (rocprofv3 children started before this
+# process touches the GPU); otherwise the committed summary supplies them.
+
+TRAFFIC_KERNEL = "qmv64_kernel<1, 1>"
+TRAFFIC_PROFILE = ROOT / "profiles" / "qmv64_decode_gate_up.traffic.txt"
+
+
+def _pmc_run(counter, only, outdir):
+    import csv
+    import subprocess
+
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", str(outdir), "-o", "run", "--",
+           sys.executable, str(ROOT / "bench.py"), "--only", only, "--eager", "--steps", "20", "--warmup", "2",
+           "--no-cpu-baseline"]
+    env = dict(os.environ, TMPDIR="/tmp")
+    subprocess.run(cmd, cwd="/tmp", env=env, check=True, timeout=90, stdout=subprocess.DEVNULL,
+                   stderr=subprocess.DEVNULL)
+    per = {}
+    for path in Path(outdir).rglob("*counter_collection.csv"):
+        for row in csv.DictReader(open(path)):
+            per.setdefault(row["Kernel_Name"], {}).setdefault(row["Dispatch_Id"], 0.0)
+            per[row["Kernel_Name"]][row["Dispatch_Id"]] += float(row["Counter_Value"])
+    return {k: sum(v.values()) / len(v) for k, v in per.items()}
+
+
+def _pick(per, needle):
+    hits = [v for k, v in per.items() if needle in k]
+    if not hits:
+        raise RuntimeError(f"no dispatch of {needle} in the counter output")
+    return hits[0]
+
+
+def measure_traffic_live():
+    """Four counter passes: FETCH_SIZE and WRITE_SIZE of the decode kernel and
+    of the calibration copy.  Bytes per launch, or None when rocprofv3 fails."""
+    import shutil
+    import tempfile
+
+    if shutil.which("rocprofv3") is None:
+        return None
+    tmp = Path(tempfile.mkdtemp(prefix="qmoe_pmc_", dir="/tmp"))
+    try:
+        f_k = _pick(_pmc_run("FETCH_SIZE", "1", tmp / "f1"), TRAFFIC_KERNEL)
+        w_k = _pick(_pmc_run("WRITE_SIZE", "1", tmp / "w1"), TRAFFIC_KERNEL)
+        f_c = _pick(_pmc_run("FETCH_SIZE", "copy", tmp / "fc"), "copyBuffer")
+        w_c = _pick(_pmc_run("WRITE_SIZE", "copy", tmp / "wc"), "copyBuffer")
+    except Exception as exc:  # noqa: BLE001 - traffic is optional
+        print(f"[bench] traffic measurement failed: {exc}", file=sys.stderr, flush=True)
+        return None
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return _traffic(f_k, w_k, f_c, w_c, "live rocprofv3 --pmc")
+
+
+def _traffic(fetch_kib, write_kib, copy_fetch_kib, copy_write_kib, source):
+    copy_bytes = CALIBRATION_MIB * 2 ** 20
+    f_scale = copy_bytes / (copy_fetch_kib * 1024)
+    w_scale = copy_bytes / (copy_write_kib * 1024)
+    return {"bytes": fetch_kib * 1024 * f_scale + write_kib * 1024 * w_scale, "fetch_kib": fetch_kib,
+            "write_kib": write_kib, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+            "source": source}
+
+
+def traffic_from_profile():
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("json: "):
+                d = json.loads(line[6:])
+                return _traffic(d["fetch_kib"], d["write_kib"], d["copy_fetch_kib"], d["copy_write_kib"],
+                                TRAFFIC_PROFILE.name)
+    except (OSError, ValueError, KeyError):
+        pass
+    return None
+
+
+def _rounds_for(k, most=8):
+    """The largest divisor of k that is at most `most`."""
+    return max(r for r in range(1, min(most, k) + 1) if k % r == 0)
+
+
 def time_graph(fn_list, warmup, dev):
-    """Capture the launches in fn_list (one per step) into a graph, replay once
-    untimed after `warmup` eager steps, then time one replay with events on
-    the replay stream.  Returns seconds per step."""
+    """Split the K launches of fn_list into R <= 8 consecutive chunks, capture
+    each chunk as a graph, run `warmup` eager steps and one untimed replay of
+    every chunk, then time one replay of each chunk with events on the replay
+    stream.  Exactly K steps are timed; consecutive chunks use different
+    weight sets.  Returns (median seconds per step, {"min", "median", "rounds"})."""
+    import statistics
+
     import torch
 
+    k = len(fn_list)
+    r = _rounds_for(k)
+    n = k // r
     for i in range(warmup):
-        fn_list[i % len(fn_list)]()
+        fn_list[i % k]()
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
+    graphs = []
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(g, stream=s):
-            for fn in fn_list:
-                fn()
+    for c in range(r):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                for fn in fn_list[c * n:(c + 1) * n]:
+                    fn()
+        graphs.append(g)
     torch.cuda.synchronize()
-    g.replay()
+    for g in graphs:
+        g.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    g.replay()
-    e1.record(st)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(r + 1)]
+    ev[0].record(st)
+    for c, g in enumerate(graphs):
+        g.replay()
+        ev[c + 1].record(st)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / len(fn_list), g
+    per = [ev[c].elapsed_time(ev[c + 1]) / 1e3 / n for c in range(r)]
+    med = statistics.median(per)
+    return med, {"min": min(per), "median": med, "rounds": r, "graphs": graphs}
 
 
 # --------------------------------------------------------------- workloads
@@ -284,8 +387,21 @@ def setup_cfg3(args, dev):
     wl, x, sets, r, lhs, out = _prefill_common(args, dev, 3)
     t = r.tiles
     steps = max(1, args.steps // 10)
+    # load-time repack into the tile layout (outside the timed region)
+    tsets = [ops.repack_tiles(w, s, b) for (w, s, b) in sets]
+    torch.cuda.synchronize()
 
-    def mk(i):
+    def mk_tiles(i):
+        tw = tsets[i % len(tsets)]
+
+        def f():
+            ops._lib.call("qmoe_gather_qmm_sorted_tiles", x.data_ptr(), lhs.data_ptr(), t.rows, 2048,
+                          tw.wp.data_ptr(), tw.sb.data_ptr(), 256, 1024, t.offsets.data_ptr(),
+                          t.tile_row.data_ptr(), t.tile_exp.data_ptr(), t.ntiles.data_ptr(), t.maxt,
+                          out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        return f
+
+    def mk_mlx(i):
         w, s, b = sets[i % len(sets)]
 
         def f():
@@ -295,11 +411,13 @@ def setup_cfg3(args, dev):
                           out.data_ptr(), torch.cuda.current_stream().cuda_stream)
         return f
 
-    return wl, [mk(i) for i in range(steps)], {
+    return wl, [mk_tiles(i) for i in range(steps)], {
         "flops": synth.algorithmic_flops(3, wl), "bound": "mfma", "peak_tflops": BF16_PEAK_TFLOPS,
-        "kernel": "gemm_bf16_kernel", "sets": len(sets),
+        "kernel": "gemm_bf16_kernel<8, true>", "sets": len(sets),
+        "alt": ("mlx_layout_us_per_call", [mk_mlx(i) for i in range(steps)]),
         "workload": "prefill grouped GEMM: 4096 tokens x top-10 Zipf(1.1) routed rows sorted by expert, "
-                    "gate_up W [256,1024,2048] int4 g64, x gathered in-kernel -> [40960,1024]"}
+                    "gate_up W [256,1024,2048] int4 g64 (tile layout, repacked at load), x gathered "
+                    "in-kernel -> [40960,1024]"}
 
 
 def setup_cfg4(args, dev):
@@ -394,6 +512,9 @@ def main():
         print(json.dumps({"error": "this path runs on one GPU; --gpus must be 1 (expert-parallel "
                                    "sharding over several GPUs is not built)"}))
         return 2
+    traffic = None
+    if args.traffic and args.only is None:
+        traffic = measure_traffic_live()  # child processes, before this one touches the GPU
     import torch
     from titan_amd import _lib
 
@@ -411,9 +532,10 @@ def main():
         print(f"[bench] workload {cfg}: setup", file=sys.stderr, flush=True)
         wl, fns, meta = SETUPS[cfg](args, dev)
         print(f"[bench] workload {cfg}: timing {len(fns)} steps", file=sys.stderr, flush=True)
-        sec, _g = (time_eager if args.eager else time_graph)(fns, args.warmup, dev)
-        res = {"workload": meta["workload"], "us_per_call": round(sec * 1e6, 3), "kernel": meta["kernel"],
-               "weight_sets": meta["sets"]}
+        sec, tinfo = (time_eager if args.eager else time_graph)(fns, args.warmup, dev)
+        res = {"workload": meta["workload"], "us_per_call": round(sec * 1e6, 3),
+               "us_per_call_min": round(tinfo["min"] * 1e6, 3), "timed_rounds": tinfo["rounds"],
+               "kernel": meta["kernel"], "weight_sets": meta["sets"]}
         if meta["bound"] == "hbm":
             gbs = meta["bytes"] / sec / 1e9
             res.update(metric="HBM GB/s", value=round(gbs, 1), bytes_per_call=meta["bytes"],
@@ -426,11 +548,16 @@ def main():
         for k_ in ("mean_distinct_experts",):
             if k_ in meta:
                 res[k_] = meta[k_]
+        if "alt" in meta:
+            label, alt = meta["alt"]
+            sec_alt, _ta = (time_eager if args.eager else time_graph)(alt, args.warmup, dev)
+            res[label] = round(sec_alt * 1e6, 3)
+            del alt, _ta
         results[cfg] = res
         print(f"[bench] workload {cfg}: {res}", file=sys.stderr, flush=True)
         if cfg == 1:
             head = (wl, meta, sec)
-        del fns, _g
+        del fns, tinfo
         torch.cuda.empty_cache()
     if args.only is not None:
         return 0
@@ -439,6 +566,8 @@ def main():
         return 0
     wl, meta, sec = head
     gbs = meta["bytes"] / sec / 1e9
+    if traffic is None:
+        traffic = traffic_from_profile()
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -451,7 +580,10 @@ def main():
         "config": {"workload": meta["workload"], "tokens": 1, "top_k": 10, "experts": 256, "hidden": 2048,
                    "intermediate": 512, "group_size": 64, "bits": 4, "weight_sets_rotated": meta["sets"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None if traffic is None else round(traffic["bytes"]),
+                     "kernel": TRAFFIC_KERNEL, "bytes_per_launch": meta["bytes"],
+                     "traffic_detail": traffic},
         "cpu_baseline": cpu,
         "configs": results,
     }

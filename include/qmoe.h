@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 1
+#define QMOE_ABI_VERSION 2
 
 enum {
   QMOE_OK = 0,
@@ -173,6 +173,36 @@ int qmoe_moe_down_wsum(const uint16_t* h, const int32_t* idx,
 int qmoe_weighted_sum(const uint16_t* xs, const int32_t* inv_order,
                       const float* scores, int64_t rows, int64_t top_k,
                       int64_t dim, int mode, uint16_t* out, void* stream);
+
+/* ----------------------------------------------------------- tile layout --
+ * Load-time repack of 4-bit, group-64 expert weights into the layout the
+ * grouped GEMMs copy contiguously: per (expert, 64-column block, group) one
+ * 2 KiB chunk of codes and one 256-byte chunk of scale/bias pairs.  Replaces,
+ * in role, the reference's per-tensor prepared tables
+ * (titan/kernels/moe_gather_int8.py:189-248 build_tables): built once per
+ * weight tensor, owned by the caller; the MLX-layout tensors stay accepted by
+ * every other entry point.  With G = K/64 and c the 64-column block:
+ *   wp[e][c][g][j][h][l][t] = w[e][64c + 32j + l][8g + 4h + t]
+ *        (j < 2, h < 2, l < 32, t < 4; as many words as w)
+ *   sb[e][c][g][i]          = s[e][64c + i][g] | b[e][64c + i][g] << 16
+ *        (i < 64; as many bytes as scales and biases together)
+ * Requires bits == 4, group_size == 64, N % 64 == 0, K % 64 == 0. */
+int qmoe_repack_tiles(const uint32_t* w, const uint16_t* scales,
+                      const uint16_t* biases, int32_t num_experts, int64_t N,
+                      int64_t K, int group_size, int bits, uint32_t* wp,
+                      uint32_t* sb, void* stream);
+
+/* qmoe_gather_qmm_sorted over tile-layout weights (wp, sb from
+ * qmoe_repack_tiles); same rows, tiles, arithmetic and summation order, so
+ * the result is bit-identical to the MLX-layout call. */
+int qmoe_gather_qmm_sorted_tiles(const uint16_t* x, const int32_t* x_rows,
+                                 int64_t n_rows, int64_t K, const uint32_t* wp,
+                                 const uint32_t* sb, int32_t num_experts,
+                                 int64_t N, const int32_t* offsets,
+                                 const int32_t* tile_row,
+                                 const int32_t* tile_exp,
+                                 const int32_t* ntiles, int64_t max_tiles,
+                                 uint16_t* out, void* stream);
 
 /* ------------------------------------------------------------------ int8 --
  * int8-activation x int4-weight gate_up (replaces

@@ -222,6 +222,8 @@ def _sorted_problem(seed, E, N, K, R, zipf=True, one_expert=False):
     (32, 512, 2048, 700, "uniform"),
     (4, 256, 1024, 500, "one"),
     (16, 1024, 1024, 64, "zipf"),
+    (16, 2048, 512, 700, "zipf"),    # the prefill down projection's shape (K = I = 512)
+    (8, 768, 384, 333, "uniform"),   # K = 3 * 128, N = 3 * 256: the four-wave column block
 ])
 def test_sorted_gemm_bf16(dev, orc, E, N, K, R, kind):
     say(f"sorted GEMM E={E} N={N} K={K} R={R} {kind}")
@@ -333,3 +335,47 @@ def test_sorted_gemm_int8_cfg4_sampled(dev, orc):
     ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, (order[rows] // k).astype(np.int32), srt[rows], wl["w"],
                                         wl["s"], wl["b"])
     assert_close_bf16(orc, bits(y)[rows], ref64, what=f"cfg4 {rows.size} rows")
+
+
+# ---------------------------------------------------------------- tile layout
+
+
+def _tile_layout_np(w, s, b):
+    """The tile layout's index map restated in numpy (the header's formulas)."""
+    E, N, KW = w.shape
+    G = KW // 8
+    wp = w.reshape(E, N // 64, 2, 32, G, 2, 4).transpose(0, 1, 4, 2, 5, 3, 6)  # e c g j h l t
+    sb = (s.astype(np.uint32) | (b.astype(np.uint32) << 16)).reshape(E, N // 64, 64, G).transpose(0, 1, 3, 2)
+    return np.ascontiguousarray(wp), np.ascontiguousarray(sb)
+
+
+@pytest.mark.parametrize("E,N,K", [(3, 64, 64), (4, 256, 512), (2, 1024, 2048)])
+def test_repack_tiles_is_the_documented_permutation(dev, E, N, K):
+    say(f"repack E={E} N={N} K={K}")
+    rng = np.random.default_rng(E * N + K)
+    w, s, b = synth.quant_weights(rng, (E, N), K)
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    want_wp, want_sb = _tile_layout_np(w, s, b)
+    got_wp = tw.wp.cpu().numpy().view(np.uint32)
+    got_sb = tw.sb.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got_wp, want_wp) and np.array_equal(got_sb, want_sb)
+
+
+@pytest.mark.parametrize("E,N,K,R,kind", [
+    (8, 256, 1024, 300, "zipf"),
+    (16, 1024, 2048, 700, "uniform"),
+    (16, 2048, 512, 500, "zipf"),
+    (8, 768, 192, 333, "one"),   # K = 3 groups: no pair constraint in the tile layout
+])
+def test_sorted_gemm_tiles_is_bit_identical_to_mlx_layout(dev, orc, E, N, K, R, kind):
+    say(f"sorted GEMM tile layout E={E} N={N} K={K} R={R} {kind}")
+    w, s, b, ids, x = _sorted_problem(E * 17 + R, E, N, K, R, zipf=kind == "zipf", one_expert=kind == "one")
+    xt = bf16_t(x, dev)
+    tiles = ops.build_tiles(i32_t(ids, dev), E)
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    y_t = ops.gather_qmm_sorted_tiles(xt, tw, tiles)
+    ref64, _ = orc.gather_qmm_rows(x, None, ids, w, s, b, deq="bf16")
+    assert_close_bf16(orc, bits(y_t), ref64, what=f"gemm tiles {E}/{N}/{K}/{R}")
+    if K % 128 == 0:
+        y_m = ops.gather_qmm_sorted(xt, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
+        assert np.array_equal(bits(y_t), bits(y_m))

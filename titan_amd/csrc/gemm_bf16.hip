@@ -57,7 +57,6 @@ struct Cfg {
   static constexpr int kSBytes = W * 2 * 64 * 4;  // [wave][scale|bias][lane] x 4 B
   static constexpr int kStageBytes = kSOff + kSBytes;
   static constexpr int kACopies = kABytes / (W * 1024);  // 16-byte-per-lane copies of A per wave
-  static constexpr int kDmaPerGroup = kACopies + 4;      // + 2 B + 2 S
   static_assert(kStages * kStageBytes * kBlocksPerCU <= 160 * 1024, "LDS per CU");
   static_assert(kStages >= 2 && kStages <= 4, "wait_group covers up to two groups in flight");
 };
@@ -70,6 +69,7 @@ struct GemmArgs {
   const uint32_t* w;
   const uint16_t* s;
   const uint16_t* b;
+  const uint32_t* sb;  // tile layout: scale|bias words (w then holds the tile-layout codes)
   int num_experts;
   int N;
   const int32_t* offsets;
@@ -150,13 +150,20 @@ __device__ __forceinline__ i32x4_t dequant_word(uint32_t v, float s, float b) {
 // over the eight rows of each parity among r..r+15).
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
+// Copies per wave and group: A, two B, and the scales and biases -- two
+// 4-byte copies (scale pair, bias pair) from the MLX layout, one (the
+// column's scale|bias word) from the tile layout.
+template <int W, bool TILED>
+constexpr int kDmaPerGroup = Cfg<W>::kACopies + 2 + (TILED ? 1 : 2);
+
 template <int W>
 struct Ctx {
   // per-lane global sources at group 0 (advance per group)
   const char* a_src[Cfg<W>::kACopies];  // activation 16-byte units, one per A copy
-  const char* b_src[2];  // packed codes of the lane's column in each subtile
-  const char* s_src;     // scale pair (groups 2j, 2j+1) of column (wave*64 + lane)
-  const char* z_src;     // bias pair
+  const char* b_src[2];  // codes of the lane's column in each subtile
+  const char* s_src;     // MLX layout: scale pair (groups 2j, 2j+1) of column (wave*64 + lane);
+                         // tile layout: scale|bias word of that column
+  const char* z_src;     // MLX layout: bias pair
   uint32_t lds;          // LDS address of the ring
   uint32_t a_dst[Cfg<W>::kACopies];  // wave-uniform LDS offsets within a stage
   uint32_t b_dst[2];
@@ -165,53 +172,68 @@ struct Ctx {
   int wave, lane, l32, h;
 };
 
-template <int W>
+template <int W, bool TILED>
 __device__ __forceinline__ void issue_group(const Ctx<W>& c, int g) {
   using C = Cfg<W>;
   const uint32_t st = c.lds + (uint32_t)(g % C::kStages) * C::kStageBytes;
 #pragma unroll
   for (int q = 0; q < C::kACopies; ++q) dma16(c.a_src[q] + (size_t)g * 128, st + c.a_dst[q]);
+  if constexpr (TILED) {
+    // one 2 KiB code chunk and one 256-byte scale|bias chunk per group
 #pragma unroll
-  for (int j = 0; j < 2; ++j) dma16(c.b_src[j] + (size_t)g * 32, st + c.b_dst[j]);
-  dma4(c.s_src + (size_t)(g >> 1) * 4, st + c.s_dst);
-  dma4(c.z_src + (size_t)(g >> 1) * 4, st + c.z_dst);
+    for (int j = 0; j < 2; ++j) dma16(c.b_src[j] + (size_t)g * 2048, st + c.b_dst[j]);
+    dma4(c.s_src + (size_t)g * 256, st + c.s_dst);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(c.b_src[j] + (size_t)g * 32, st + c.b_dst[j]);
+    dma4(c.s_src + (size_t)(g >> 1) * 4, st + c.s_dst);
+    dma4(c.z_src + (size_t)(g >> 1) * 4, st + c.z_dst);
+  }
 }
 
 // Wait until this wave's copies of group g have landed: the copies of the
 // groups issued after it (at most kStages - 2, each kDmaPerGroup copies)
 // may stay in flight.
-template <int W>
+template <int D>
 __device__ __forceinline__ void wait_group(int ahead) {
-  constexpr int D = Cfg<W>::kDmaPerGroup;
   if (ahead >= 2) wait_vmem<2 * D>();
   else if (ahead == 1) wait_vmem<D>();
   else wait_vmem<0>();
 }
 
-template <int W, int MSUB>
+template <int W, bool TILED, int MSUB>
 __device__ __forceinline__ void tile_loop(const Ctx<W>& c, const char* smem, f32x16_t (&acc)[4][2]) {
   using C = Cfg<W>;
   constexpr int kStages = C::kStages, kAOff = C::kAOff, kBOff = C::kBOff, kSOff = C::kSOff;
   const int G = c.G;
 #pragma unroll
   for (int d = 0; d < kStages - 1; ++d)
-    if (d < G) issue_group(c, d);
+    if (d < G) issue_group<W, TILED>(c, d);
 
   for (int g = 0; g < G; ++g) {
-    wait_group<W>(min(kStages - 2, G - 1 - g));
+    wait_group<kDmaPerGroup<W, TILED>>(min(kStages - 2, G - 1 - g));
     __builtin_amdgcn_s_barrier();
-    if (g + kStages - 1 < G) issue_group(c, g + kStages - 1);
+    if (g + kStages - 1 < G) issue_group<W, TILED>(c, g + kStages - 1);
 
     const char* st = smem + (g % kStages) * C::kStageBytes;
     // this lane's codes, scales and biases for its two columns
     const uint4 raw0 = *reinterpret_cast<const uint4*>(st + kBOff + (c.wave * 2 + 0) * 1024 + c.lane * 16);
     const uint4 raw1 = *reinterpret_cast<const uint4*>(st + kBOff + (c.wave * 2 + 1) * 1024 + c.lane * 16);
     const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + kSOff + c.wave * 512);
-    const int sh = (g & 1) ? 16 : 0;
-    const float s0 = __uint_as_float((sw[c.l32] >> sh) << 16);
-    const float s1 = __uint_as_float((sw[c.l32 + 32] >> sh) << 16);
-    const float z0 = __uint_as_float((sw[64 + c.l32] >> sh) << 16);
-    const float z1 = __uint_as_float((sw[64 + c.l32 + 32] >> sh) << 16);
+    float s0, s1, z0, z1;
+    if constexpr (TILED) {
+      const uint32_t v0 = sw[c.l32], v1 = sw[c.l32 + 32];
+      s0 = __uint_as_float(v0 << 16);
+      z0 = __uint_as_float(v0 & 0xFFFF0000u);
+      s1 = __uint_as_float(v1 << 16);
+      z1 = __uint_as_float(v1 & 0xFFFF0000u);
+    } else {
+      const int sh = (g & 1) ? 16 : 0;
+      s0 = __uint_as_float((sw[c.l32] >> sh) << 16);
+      s1 = __uint_as_float((sw[c.l32 + 32] >> sh) << 16);
+      z0 = __uint_as_float((sw[64 + c.l32] >> sh) << 16);
+      z1 = __uint_as_float((sw[64 + c.l32 + 32] >> sh) << 16);
+    }
     const uint32_t w0[4] = {raw0.x, raw0.y, raw0.z, raw0.w};
     const uint32_t w1[4] = {raw1.x, raw1.y, raw1.z, raw1.w};
     const char* abuf = st + kAOff;
@@ -237,7 +259,7 @@ __device__ __forceinline__ void tile_loop(const Ctx<W>& c, const char* smem, f32
   }
 }
 
-template <int W>
+template <int W, bool TILED>
 __global__ __launch_bounds__(Cfg<W>::kThreads, Cfg<W>::kBlocksPerCU) void gemm_bf16_kernel(GemmArgs a) {
   using C = Cfg<W>;
   constexpr int kBN = C::kBN, kWaves = C::kWaves;
@@ -288,12 +310,22 @@ __global__ __launch_bounds__(Cfg<W>::kThreads, Cfg<W>::kBlocksPerCU) void gemm_b
   }
   const int64_t col_base = (int64_t)e * a.N + nblk * kBN + c.wave * 64;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    c.b_src[j] = reinterpret_cast<const char*>(a.w + (col_base + j * 32 + c.l32) * KW + c.h * 4);
-    c.b_dst[j] = (uint32_t)(C::kBOff + (c.wave * 2 + j) * 1024);
+  for (int j = 0; j < 2; ++j) c.b_dst[j] = (uint32_t)(C::kBOff + (c.wave * 2 + j) * 1024);
+  if constexpr (TILED) {
+    // chunk (e, c, g) of the tile layout, c = the wave's 64-column block
+    const int64_t chunk0 = ((int64_t)e * (a.N / 64) + nblk * kWaves + c.wave) * G;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      c.b_src[j] = reinterpret_cast<const char*>(a.w) + (chunk0 * 2 + j) * 1024 + c.lane * 16;
+    c.s_src = reinterpret_cast<const char*>(a.sb) + chunk0 * 256 + c.lane * 4;
+    c.z_src = nullptr;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      c.b_src[j] = reinterpret_cast<const char*>(a.w + (col_base + j * 32 + c.l32) * KW + c.h * 4);
+    c.s_src = reinterpret_cast<const char*>(a.s + (col_base + c.lane) * G);
+    c.z_src = reinterpret_cast<const char*>(a.b + (col_base + c.lane) * G);
   }
-  c.s_src = reinterpret_cast<const char*>(a.s + (col_base + c.lane) * G);
-  c.z_src = reinterpret_cast<const char*>(a.b + (col_base + c.lane) * G);
   c.s_dst = (uint32_t)(C::kSOff + c.wave * 512);
   c.z_dst = c.s_dst + 256;
 
@@ -306,10 +338,10 @@ __global__ __launch_bounds__(Cfg<W>::kThreads, Cfg<W>::kBlocksPerCU) void gemm_b
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   switch (msub) {
-    case 1: tile_loop<W, 1>(c, smem, acc); break;
-    case 2: tile_loop<W, 2>(c, smem, acc); break;
-    case 3: tile_loop<W, 3>(c, smem, acc); break;
-    default: tile_loop<W, 4>(c, smem, acc); break;
+    case 1: tile_loop<W, TILED, 1>(c, smem, acc); break;
+    case 2: tile_loop<W, TILED, 2>(c, smem, acc); break;
+    case 3: tile_loop<W, TILED, 3>(c, smem, acc); break;
+    default: tile_loop<W, TILED, 4>(c, smem, acc); break;
   }
 
   // epilogue: D[m][n] of a 32x32 subtile sits in lane n (mod 32), register
@@ -334,36 +366,70 @@ __global__ __launch_bounds__(Cfg<W>::kThreads, Cfg<W>::kBlocksPerCU) void gemm_b
 
 extern "C" int qmoe_gemm_tile_rows(void) { return kBM; }
 
+namespace {
+
+int launch_gemm(const GemmArgs& a, int64_t max_tiles, bool tiled, void* stream) {
+  const bool wide = a.N % Cfg<8>::kBN == 0;
+  const int64_t blocks = max_tiles * (a.N / (wide ? Cfg<8>::kBN : Cfg<4>::kBN));
+  if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
+  const dim3 grid((unsigned)blocks);
+  hipStream_t st = qmoe::as_stream(stream);
+  if (wide && tiled) gemm_bf16_kernel<8, true><<<grid, dim3(Cfg<8>::kThreads), 0, st>>>(a);
+  else if (wide) gemm_bf16_kernel<8, false><<<grid, dim3(Cfg<8>::kThreads), 0, st>>>(a);
+  else if (tiled) gemm_bf16_kernel<4, true><<<grid, dim3(Cfg<4>::kThreads), 0, st>>>(a);
+  else gemm_bf16_kernel<4, false><<<grid, dim3(Cfg<4>::kThreads), 0, st>>>(a);
+  return qmoe::launch_status("gemm_bf16_kernel");
+}
+
+int check_common(const uint16_t* x, int64_t n_rows, int64_t K, int32_t num_experts, int64_t N,
+                 const int32_t* offsets, const int32_t* tile_row, const int32_t* tile_exp, const int32_t* ntiles,
+                 int64_t max_tiles, const uint16_t* out) {
+  if (n_rows < 0 || K <= 0 || N <= 0 || num_experts <= 0 || max_tiles < 0)
+    return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (n_rows == 0 || max_tiles == 0) return QMOE_OK;
+  if (!x || !offsets || !tile_row || !tile_exp || !ntiles || !out) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (N % 256) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of 256", (long long)N);
+  if (!qmoe::aligned16(x)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x must be 16-byte aligned");
+  if (K > 0x7FFFFFFF || N > 0x7FFFFFFF || n_rows > 0x7FFFFFFF)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
+  return QMOE_OK;
+}
+
+}  // namespace
+
 extern "C" int qmoe_gather_qmm_sorted(const uint16_t* x, const int32_t* x_rows, int64_t n_rows, int64_t K,
                                       const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                                       int32_t num_experts, int64_t N, int group_size, int bits,
                                       const int32_t* offsets, const int32_t* tile_row,
                                       const int32_t* tile_exp, const int32_t* ntiles, int64_t max_tiles,
                                       uint16_t* out, void* stream) {
-  if (n_rows < 0 || K <= 0 || N <= 0 || num_experts <= 0 || max_tiles < 0)
-    return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
-  if (n_rows == 0 || max_tiles == 0) return QMOE_OK;
-  if (!x || !w || !scales || !biases || !offsets || !tile_row || !tile_exp || !ntiles || !out)
-    return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  const int rc = check_common(x, n_rows, K, num_experts, N, offsets, tile_row, tile_exp, ntiles, max_tiles, out);
+  if (rc != QMOE_OK || n_rows == 0 || max_tiles == 0) return rc;
+  if (!w || !scales || !biases) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
   if (bits != 4 || group_size != 64)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sorted GEMM takes 4-bit codes with group_size 64 (got %d, %d)",
                       bits, group_size);
   // scales and biases are copied in pairs of groups: K / 64 must be even
   if (K % 128) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 128", (long long)K);
-  if (N % 256) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of 256", (long long)N);
-  if (!qmoe::aligned16(x) || !qmoe::aligned16(w) || !qmoe::aligned16(scales) || !qmoe::aligned16(biases))
-    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x, w, scales and biases must be 16-byte aligned");
-  if (K > 0x7FFFFFFF || N > 0x7FFFFFFF || n_rows > 0x7FFFFFFF)
-    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
-  const bool wide = N % Cfg<8>::kBN == 0;
-  const int64_t blocks = max_tiles * (N / (wide ? Cfg<8>::kBN : Cfg<4>::kBN));
-  if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
-  GemmArgs a{x, x_rows, n_rows, (int)K, w, scales, biases, num_experts, (int)N, offsets, tile_row, tile_exp, ntiles,
-             out};
-  hipStream_t st = qmoe::as_stream(stream);
-  if (wide)
-    gemm_bf16_kernel<8><<<dim3((unsigned)blocks), dim3(Cfg<8>::kThreads), 0, st>>>(a);
-  else
-    gemm_bf16_kernel<4><<<dim3((unsigned)blocks), dim3(Cfg<4>::kThreads), 0, st>>>(a);
-  return qmoe::launch_status("gemm_bf16_kernel");
+  if (!qmoe::aligned16(w) || !qmoe::aligned16(scales) || !qmoe::aligned16(biases))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "w, scales and biases must be 16-byte aligned");
+  GemmArgs a{x, x_rows, n_rows, (int)K, w, scales, biases, nullptr, num_experts, (int)N, offsets, tile_row,
+             tile_exp, ntiles, out};
+  return launch_gemm(a, max_tiles, false, stream);
+}
+
+extern "C" int qmoe_gather_qmm_sorted_tiles(const uint16_t* x, const int32_t* x_rows, int64_t n_rows, int64_t K,
+                                            const uint32_t* wp, const uint32_t* sb, int32_t num_experts,
+                                            int64_t N, const int32_t* offsets, const int32_t* tile_row,
+                                            const int32_t* tile_exp, const int32_t* ntiles, int64_t max_tiles,
+                                            uint16_t* out, void* stream) {
+  const int rc = check_common(x, n_rows, K, num_experts, N, offsets, tile_row, tile_exp, ntiles, max_tiles, out);
+  if (rc != QMOE_OK || n_rows == 0 || max_tiles == 0) return rc;
+  if (!wp || !sb) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (K % 64) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 64", (long long)K);
+  if (!qmoe::aligned16(wp) || !qmoe::aligned16(sb))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "wp and sb must be 16-byte aligned");
+  GemmArgs a{x, x_rows, n_rows, (int)K, wp, nullptr, nullptr, sb, num_experts, (int)N, offsets, tile_row,
+             tile_exp, ntiles, out};
+  return launch_gemm(a, max_tiles, true, stream);
 }

@@ -93,3 +93,69 @@ extern "C" int qmoe_dequantize(const uint32_t* w, const uint16_t* scales, const 
       w, scales, biases, rows, K, group_size, bits, out);
   return qmoe::launch_status("dequant_kernel");
 }
+
+// ------------------------------------------------------------ tile repack
+
+namespace {
+
+// One thread per 16-byte unit of wp, in wp order (coalesced stores): unit
+// u = ((((e*NC + c)*G + g)*2 + j)*2 + h)*32 + l holds words 8g + 4h .. +3 of
+// row 64c + 32j + l of expert e.
+__global__ void repack_codes_kernel(const uint4* __restrict__ w, uint4* __restrict__ wp, int64_t units, int64_t N,
+                                    int NC, int G) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= units) return;
+  const int l = (int)(u & 31), h = (int)((u >> 5) & 1), j = (int)((u >> 6) & 1);
+  const int64_t q = u >> 7;
+  const int g = (int)(q % G);
+  const int64_t ec = q / G;
+  const int c = (int)(ec % NC);
+  const int64_t e = ec / NC;
+  const int64_t row = e * N + (int64_t)c * 64 + j * 32 + l;
+  wp[u] = w[row * (2 * (int64_t)G) + g * 2 + h];
+}
+
+// One thread per scale|bias word, in sb order: v = ((e*NC + c)*G + g)*64 + i.
+__global__ void repack_sb_kernel(const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
+                                 uint32_t* __restrict__ sb, int64_t words, int64_t N, int NC, int G) {
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= words) return;
+  const int i = (int)(v & 63);
+  const int64_t q = v >> 6;
+  const int g = (int)(q % G);
+  const int64_t ec = q / G;
+  const int c = (int)(ec % NC);
+  const int64_t e = ec / NC;
+  const int64_t idx = (e * N + (int64_t)c * 64 + i) * G + g;
+  sb[v] = (uint32_t)s[idx] | ((uint32_t)b[idx] << 16);
+}
+
+}  // namespace
+
+extern "C" int qmoe_repack_tiles(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                                 int32_t num_experts, int64_t N, int64_t K, int group_size, int bits, uint32_t* wp,
+                                 uint32_t* sb, void* stream) {
+  if (num_experts < 0 || N < 0 || K < 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if ((int64_t)num_experts * N * K == 0) return QMOE_OK;
+  if (!w || !scales || !biases || !wp || !sb) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (bits != 4 || group_size != 64)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "the tile layout takes 4-bit codes with group_size 64 (got %d, %d)", bits,
+                      group_size);
+  if (N % 64 || K % 64) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld, K=%lld: both must be multiples of 64",
+                                          (long long)N, (long long)K);
+  if (!qmoe::aligned16(w) || !qmoe::aligned16(wp)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "w and wp must be 16-byte aligned");
+  const int64_t G = K / 64, NC = N / 64;
+  if (G > 0x7FFFFFFF || NC > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
+  const int64_t units = (int64_t)num_experts * N * G * 2;  // 16-byte units: 32 bytes per (row, group)
+  const int64_t words = (int64_t)num_experts * N * G;
+  hipStream_t st = qmoe::as_stream(stream);
+  const int64_t bu = (units + 255) / 256, bw = (words + 255) / 256;
+  if (bu > 0x7FFFFFFF || bw > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "too many words");
+  repack_codes_kernel<<<dim3((unsigned)bu), dim3(256), 0, st>>>(reinterpret_cast<const uint4*>(w),
+                                                                 reinterpret_cast<uint4*>(wp), units, N, (int)NC,
+                                                                 (int)G);
+  int rc = qmoe::launch_status("repack_codes_kernel");
+  if (rc != QMOE_OK) return rc;
+  repack_sb_kernel<<<dim3((unsigned)bw), dim3(256), 0, st>>>(scales, biases, sb, words, N, (int)NC, (int)G);
+  return qmoe::launch_status("repack_sb_kernel");
+}

@@ -256,6 +256,61 @@ def gather_qmm_sorted(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bi
     return out
 
 
+@dataclass(frozen=True)
+class TileWeights:
+    """Expert weights repacked into the tile layout (qmoe_repack_tiles): per
+    (expert, 64-column block, group) a 2 KiB chunk of codes ``wp`` and a
+    256-byte chunk of scale|bias words ``sb``.  Built once per weight tensor
+    at load time and owned by the caller, in the role of the reference's
+    prepared tables (titan/kernels/moe_gather_int8.py:189-248)."""
+
+    wp: torch.Tensor  # int32 [E, N/64, G, 2, 2, 32, 4]
+    sb: torch.Tensor  # int32 [E, N/64, G, 64]
+    num_experts: int
+    N: int
+    K: int
+    group_size: int = GROUP
+    bits: int = BITS
+
+    @property
+    def nbytes(self) -> int:
+        return self.wp.numel() * 4 + self.sb.numel() * 4
+
+
+def repack_tiles(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = GROUP,
+                 bits: int = BITS) -> TileWeights:
+    """MLX-layout expert weights [E, N, K/8] -> :class:`TileWeights`."""
+    w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    if w.dim() != 3:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"w must be [E, N, K/8], got {tuple(w.shape)}")
+    E, N, KW = w.shape
+    K = KW * 32 // bits
+    _check_quant(w, scales, group_size, bits, K)
+    G = K // group_size
+    wp = torch.empty(E, max(N // 64, 0), G, 2, 2, 32, 4, dtype=torch.int32, device=w.device)
+    sb = torch.empty(E, max(N // 64, 0), G, 64, dtype=torch.int32, device=w.device)
+    _lib.call("qmoe_repack_tiles", w.data_ptr(), scales.data_ptr(), biases.data_ptr(), E, N, K, group_size, bits,
+              wp.data_ptr(), sb.data_ptr(), _stream(w))
+    return TileWeights(wp, sb, E, N, K, group_size, bits)
+
+
+def gather_qmm_sorted_tiles(x: torch.Tensor, tw: TileWeights, tiles: TileTable,
+                            x_rows: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`gather_qmm_sorted` over tile-layout weights; bit-identical result."""
+    x = _bf16(x, "x")
+    K = x.shape[-1]
+    if K != tw.K:
+        raise ValueError(f"x has K={K}, the weights K={tw.K}")
+    if tiles.num_experts != tw.num_experts or tiles.tile_rows != tile_rows():
+        raise ValueError("tile table does not match this call")
+    xr = None if x_rows is None else _i32(x_rows.reshape(-1), "x_rows", x.device)
+    out = torch.empty(tiles.rows, tw.N, dtype=torch.bfloat16, device=x.device)
+    _lib.call("qmoe_gather_qmm_sorted_tiles", x.data_ptr(), _ptr(xr), tiles.rows, K, tw.wp.data_ptr(),
+              tw.sb.data_ptr(), tw.num_experts, tw.N, tiles.offsets.data_ptr(), tiles.tile_row.data_ptr(),
+              tiles.tile_exp.data_ptr(), tiles.ntiles.data_ptr(), tiles.maxt, out.data_ptr(), _stream(x))
+    return out
+
+
 def gemm_supported(K: int, N: int, group_size: int, bits: int) -> bool:
     return bits == 4 and group_size == 64 and K % 128 == 0 and N % 256 == 0
 
@@ -444,7 +499,8 @@ def gather_qmm_int8_sorted(xi: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, 
 
 
 __all__ = [
-    "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "Routing", "build_tiles", "route",
+    "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "TileWeights", "Routing", "build_tiles", "route",
+    "repack_tiles", "gather_qmm_sorted_tiles",
     "max_tiles", "tile_rows", "unpack", "dequantize", "gather_qmv", "gather_qmm_sorted", "gather_qmm",
     "gemm_supported", "quantized_matmul", "gate_up_silu", "down_wsum", "moe_weighted_sum",
     "quantize_act_int8", "gather_qmm_int8_sorted",
