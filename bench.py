@@ -143,7 +143,7 @@ def calibration_copy(dev, mib=CALIBRATION_MIB, reps=5):
 # `--traffic` measures them live (rocprofv3 children started before this
 # process touches the GPU); otherwise the committed summary supplies them.
 
-TRAFFIC_KERNEL = "qmv64_kernel<1, 1>"
+TRAFFIC_KERNEL = "qmv64_kernel<1, 1, 2>"
 TRAFFIC_PROFILE = ROOT / "profiles" / "qmv64_decode_gate_up.traffic.txt"
 
 
@@ -287,8 +287,21 @@ def setup_cfg1(args, dev):
         cursor[si] += 10
     idxs[0] = to_dev(wl["idx"], "i32", dev)
     outs = [torch.empty(1, 10, 512, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    # load-time repack into the tile layout (outside the timed region)
+    tsets = [ops.repack_tiles(w, s, b) for (w, s, b) in sets]
+    torch.cuda.synchronize()
 
-    def mk(i):
+    def mk_tiles(i):
+        tw = tsets[i % len(tsets)]
+        idx = idxs[i]
+
+        def f():
+            ops._lib.call("qmoe_moe_gate_up_swiglu_tiles", x.data_ptr(), idx.data_ptr(), 1, 10, 2048,
+                          tw.wp.data_ptr(), tw.sb.data_ptr(), 256, 512, outs[i % 2].data_ptr(),
+                          torch.cuda.current_stream().cuda_stream)
+        return f
+
+    def mk_mlx(i):
         w, s, b = sets[i % len(sets)]
         idx = idxs[i]
 
@@ -298,9 +311,10 @@ def setup_cfg1(args, dev):
                           torch.cuda.current_stream().cuda_stream)
         return f
 
-    return wl, [mk(i) for i in range(args.steps)], {
+    return wl, [mk_mlx(i) for i in range(args.steps)], {
         "bytes": synth.algorithmic_bytes(1), "flops": synth.algorithmic_flops(1), "bound": "hbm",
-        "kernel": "qmv64_kernel<1,1>", "sets": len(sets),
+        "kernel": "qmv64_kernel<1,1,2>", "sets": len(sets),
+        "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(args.steps)]),
         "workload": "decode gate_up gather_qmm + SwiGLU: 1 token, H=2048, E=256, top_k=10, "
                     "W [256,1024,2048] int4 g64 bf16 scale/bias -> h [10,512]"}
 
@@ -313,8 +327,18 @@ def setup_cfg0(args, dev):
     sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 100)
     x = to_dev(wl["x"], "bf16", dev)
     out = torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)
+    tsets = [ops.repack_tiles(w[None], s[None], b[None]) for (w, s, b) in sets]
+    torch.cuda.synchronize()
 
-    def mk(i):
+    def mk_tiles(i):
+        tw = tsets[i % len(tsets)]
+
+        def f():
+            ops._lib.call("qmoe_gather_qmv_tiles", x.data_ptr(), None, None, 1, 2048, tw.wp.data_ptr(),
+                          tw.sb.data_ptr(), 1, 4096, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        return f
+
+    def mk_mlx(i):
         w, s, b = sets[i % len(sets)]
 
         def f():
@@ -322,9 +346,10 @@ def setup_cfg0(args, dev):
                           b.data_ptr(), 4096, 64, 4, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
         return f
 
-    return wl, [mk(i) for i in range(args.steps)], {
+    return wl, [mk_mlx(i) for i in range(args.steps)], {
         "bytes": synth.algorithmic_bytes(0), "flops": synth.algorithmic_flops(0), "bound": "hbm",
-        "kernel": "qmv64_kernel<1,0>", "sets": len(sets),
+        "kernel": "qmv64_kernel<1,0,2>", "sets": len(sets),
+        "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(args.steps)]),
         "workload": "dense quantized_matmul x [1,2048] . W [4096,2048] int4 g64"}
 
 

@@ -204,6 +204,22 @@ int qmoe_gather_qmm_sorted_tiles(const uint16_t* x, const int32_t* x_rows,
                                  const int32_t* ntiles, int64_t max_tiles,
                                  uint16_t* out, void* stream);
 
+/* Decode gather-GEMV (qmoe_gather_qmv) and the fused gate_up + SwiGLU
+ * (qmoe_moe_gate_up_swiglu) over tile-layout weights; same results as the
+ * MLX-layout calls (the same factored arithmetic and reduction order), with
+ * the scale|bias words of four rows read in one 16-byte load.  Requires
+ * K = 2048*n (n <= 4) and 64 | rows per expert; I % 4 == 0 for the SwiGLU form. */
+int qmoe_gather_qmv_tiles(const uint16_t* x, const int32_t* x_rows,
+                          const int32_t* experts, int64_t n_rows, int64_t K,
+                          const uint32_t* wp, const uint32_t* sb,
+                          int32_t num_experts, int64_t N, uint16_t* out,
+                          void* stream);
+int qmoe_moe_gate_up_swiglu_tiles(const uint16_t* x, const int32_t* idx,
+                                  int64_t T, int64_t top_k, int64_t K,
+                                  const uint32_t* wp, const uint32_t* sb,
+                                  int32_t num_experts, int64_t I, uint16_t* h,
+                                  void* stream);
+
 /* ------------------------------------------------------------------ int8 --
  * int8-activation x int4-weight gate_up (replaces
  * titan/kernels/moe_gather_int8.py:132-182 quantize_activations and

@@ -41,8 +41,10 @@ def gather_sorted():
     w, s, b = synth.quant_weights(rng, (E, N), K)
     ids = np.sort(rng.integers(0, E, size=R)).astype(np.int32)
     x = synth.bf16_bits(rng.normal(size=(R, K)).astype(np.float32))
+    # materialised bf16 weights (the grouped GEMM) and the exact affine form (the GEMV)
     y64, y16 = oracle.gather_qmm_rows(x, None, ids, w, s, b, deq="bf16")
-    _save("gather_sorted", w=w, s=s, b=b, ids=ids, x=x, y64=y64, y16=y16)
+    e64, _ = oracle.gather_qmm_rows(x, None, ids, w, s, b, deq="exact")
+    _save("gather_sorted", w=w, s=s, b=b, ids=ids, x=x, y64=y64, y16=y16, e64=e64)
 
 
 def decode_gate_up():

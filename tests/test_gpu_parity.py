@@ -379,3 +379,50 @@ def test_sorted_gemm_tiles_is_bit_identical_to_mlx_layout(dev, orc, E, N, K, R, 
     if K % 128 == 0:
         y_m = ops.gather_qmm_sorted(xt, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
         assert np.array_equal(bits(y_t), bits(y_m))
+
+
+def test_gate_up_swiglu_tiles_cfg1_matches_mlx_layout(dev, orc):
+    say("gate_up + SwiGLU tile layout, workload 1")
+    wl = synth.make(1)
+    w, s, b = words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev)
+    tw = ops.repack_tiles(w, s, b)
+    idx = i32_t(wl["idx"], dev)
+    h_t = ops.gate_up_silu_tiles(bf16_t(wl["x"], dev), tw, idx)
+    h_m = ops.gate_up_silu(bf16_t(wl["x"], dev), w, s, b, idx)
+    assert np.array_equal(bits(h_t), bits(h_m))
+    gu64, _ = orc.gather_qmm_rows(wl["x"], np.zeros(10, np.int32), wl["idx"].reshape(-1), wl["w"],
+                                  wl["s"], wl["b"])
+    h64, _ = orc.swiglu(gu64)
+    assert_close_bf16(orc, bits(h_t).reshape(10, 512), h64, what="cfg1 swiglu tiles")
+
+
+@pytest.mark.parametrize("T,k,E,I,K", [(3, 4, 16, 96, 2048), (1, 10, 16, 256, 4096), (2, 2, 4, 64, 6144)])
+def test_gate_up_swiglu_tiles_shapes(dev, orc, T, k, E, I, K):
+    say(f"gate_up tiles T={T} k={k} E={E} I={I} K={K}")
+    rng = np.random.default_rng(T * 1000 + K)
+    w, s, b = synth.quant_weights(rng, (E, 2 * I), K)
+    x = synth.bf16_bits(rng.normal(size=(T, K)).astype(np.float32))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    h = ops.gate_up_silu_tiles(bf16_t(x, dev), tw, i32_t(idx, dev))
+    rows = np.repeat(np.arange(T, dtype=np.int32), k)
+    gu64, _ = orc.gather_qmm_rows(x, rows, idx.reshape(-1), w, s, b)
+    h64, _ = orc.swiglu(gu64)
+    assert_close_bf16(orc, bits(h).reshape(T * k, I), h64, what=f"gate_up tiles {T}/{k}/{E}/{I}/{K}")
+
+
+@pytest.mark.parametrize("R,E,N,K", [(1, 1, 4096, 2048), (7, 8, 192, 4096), (5, 3, 64, 8192)])
+def test_gather_qmv_tiles(dev, orc, R, E, N, K):
+    say(f"gather_qmv tiles R={R} E={E} N={N} K={K}")
+    rng = np.random.default_rng(R * 7 + N)
+    w, s, b = synth.quant_weights(rng, (E, N), K)
+    x = synth.bf16_bits(rng.normal(size=(3, K)).astype(np.float32))
+    xr = rng.integers(0, 3, size=R).astype(np.int32)
+    ex = rng.integers(0, E, size=R).astype(np.int32)
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    y = ops.gather_qmv_tiles(bf16_t(x, dev), i32_t(xr, dev), i32_t(ex, dev), tw)
+    ref64, _ = orc.gather_qmm_rows(x, xr, ex, w, s, b)
+    assert_close_bf16(orc, bits(y), ref64, what=f"qmv tiles {R}/{E}/{N}/{K}")
+    ym = ops.gather_qmv(bf16_t(x, dev), i32_t(xr, dev), i32_t(ex, dev), words_t(w, dev), bf16_t(s, dev),
+                        bf16_t(b, dev))
+    assert np.array_equal(bits(y), bits(ym))

@@ -22,6 +22,12 @@ namespace {
 
 constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
 
+// Rows per row group of the 2048-chunk GEMV (see qmv64_kernel): 2 gives each
+// wave two gate/up pairs, twice as many waves as 4.
+#ifndef QMOE_QMV_RG
+#define QMOE_QMV_RG 2
+#endif
+
 // x pairs laid out to match the nibble pairs of one 32-bit code word:
 // word j covers elements 8j..8j+7; pairs are (0,4), (1,5), (2,6), (3,7).
 struct XChunk {
@@ -80,6 +86,7 @@ struct QmvArgs {
   int n_out;  // outputs per pair (N, or I for the SwiGLU form)
   int n_w;    // weight rows per expert (N, or 2I)
   uint16_t* out;
+  const uint32_t* sb;  // tile layout: scale|bias words (w then holds the tile-layout codes)
 };
 
 // MODE 0: out[r, n] = x_row . W[e][n]
@@ -193,10 +200,121 @@ __device__ __forceinline__ uint4 load_nt(const uint4* p) {
   return make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
 }
 
-// MODE 0: eight outputs per wave; MODE 1: four gate/up pairs per wave.
-template <int NV, int MODE>
+// A wave computes two row groups of RG consecutive rows (RG = 4 or 2):
+// MODE 0 rows n0.. and n0 + RG.. (2*RG outputs); MODE 1 gate rows n0.. and up
+// rows n_out + n0.. (RG SwiGLU outputs).  Row i of group g sits in partial
+// slot 4g + i, so the transposed eight-slot reduction leaves row 4g + i in
+// lanes 8(4g + i).. and each up row 32 lanes above its gate row.
+// Scales and biases of the wave's rows -- four segments [array][group][RG rows][G]
+// bf16 taken from the MLX arrays, RG*G/2 16-byte units -- are fetched with
+// one load per lane and unit, staged once in LDS, and read back per lane for
+// its own group.  Loads are issued in the order they are consumed: x, the
+// scales and biases, then the codes row by row; x goes first because it does
+// not wait for the expert id.
+template <int NV, int MODE, int RG>
 __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
+  constexpr int OUTS = MODE == 1 ? RG : 2 * RG;
+  constexpr int kMaxUnits = (RG * NV + 1) / 2;  // units per lane at group size 32 (G = 64*NV)
+  __shared__ __attribute__((aligned(16))) uint16_t sbl[4 * RG * 64 * NV];  // [seg][row][G], G <= 64*NV
+  const int lane = threadIdx.x;
+  const int64_t nblk = (a.n_out + OUTS - 1) / OUTS;
+  const int64_t r = blockIdx.x / nblk;
+  if (r >= a.n_pairs) return;
+  const int n0 = (int)(blockIdx.x % nblk) * OUTS;
+  const int64_t xr = a.x_rows ? (int64_t)a.x_rows[r] : r / a.x_div;
+  const uint16_t* xrow = a.x + xr * a.x_stride;
+  XChunk xc[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) load_x_chunk(xrow + v * 2048 + lane * 32, xc[v]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  int e = a.experts ? a.experts[r] : 0;
+  e = min(max(e, 0), a.num_experts - 1);
+  const int K = a.K;
+  const int G = K / a.group_size;
+  const int64_t KW = K / 8;
+  const int64_t ebase = (int64_t)e * a.n_w;
+  const int grp1 = MODE == 1 ? a.n_out + n0 : n0 + RG;
+  // row of slot (group g, row i), clamped into the expert (slots past n_out are computed, not stored)
+  auto row_of = [&](int g, int i) -> int64_t {
+    const int n = (g == 0 ? n0 : grp1) + i;
+    const int lim = MODE == 1 ? (g == 0 ? a.n_out - 1 : 2 * a.n_out - 1) : a.n_out - 1;
+    return ebase + min(n, lim);
+  };
+
+  const int upr = G / 8;         // 16-byte units per row
+  const int units = 4 * RG * upr;
+  // every lane loads kMaxUnits units (a clamped index repeats the last one) so the
+  // array stays in registers; only the LDS store below is predicated
+  i32x4_t sbv[kMaxUnits];
+#pragma unroll
+  for (int j = 0; j < kMaxUnits; ++j) {
+    const int u = min(lane + 64 * j, units - 1);
+    const int seg = u / (RG * upr), rem = u % (RG * upr);
+    const uint16_t* base = (seg >> 1) ? a.b : a.s;
+    sbv[j] = *reinterpret_cast<const i32x4_t*>(base + row_of(seg & 1, rem / upr) * G + (rem % upr) * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 wv[2][RG][NV];
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int i = 0; i < RG; ++i) {
+      const uint4* p = reinterpret_cast<const uint4*>(a.w + row_of(g, i) * KW) + lane;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) wv[g][i][v] = load_nt(p + v * 64);
+    }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < kMaxUnits; ++j) {
+    const int u = lane + 64 * j;
+    if (u < units) *reinterpret_cast<i32x4_t*>(sbl + u * 8) = sbv[j];
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the staged words are visible to the wave
+  __builtin_amdgcn_wave_barrier();
+  float part[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) part[q] = 0.f;
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int i = 0; i < RG; ++i) {
+      float acc = 0.f;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int gi = (v * 2048 + lane * 32) / a.group_size;
+        const float sv = bf16_to_f32(sbl[((0 * 2 + g) * RG + i) * G + gi]);
+        const float bv = bf16_to_f32(sbl[((1 * 2 + g) * RG + i) * G + gi]);
+        acc += affine_chunk(dot_chunk(wv[g][i][v], xc[v]), xc[v].sum, sv, bv);
+      }
+      part[4 * g + i] = acc;
+    }
+  const float t = reduce8(part, lane);  // lanes 8q..: slot q
+  const int q = lane >> 3;
+  if (MODE == 1) {
+    // gate slot q (< 4) in lanes 8q, its up slot 4 + q in lanes 8q + 32
+    auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
+    const float up = as_f(sw[1]);
+    if (lane < 32 && (lane & 7) == 0 && q < RG && n0 + q < a.n_out)
+      a.out[r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t / (1.0f + expf(-t)) * up);
+  } else {
+    const int g = q >> 2, i = q & 3;
+    const int n = (g == 0 ? n0 : grp1) + i;
+    if ((lane & 7) == 0 && i < RG && n < a.n_out) a.out[r * a.n_out + n] = (uint16_t)f32_to_bf16(t);
+  }
+}
+
+// qmv64 over tile-layout weights (group 64): the code chunk of row n for
+// group g, half h is 16 bytes at ((((e*NC + n/64)*G + g)*2 + (n%64)/32)*2 + h)*32
+// + n%32, so the four consecutive rows a wave reads at one (g, h) form one
+// 64-byte segment; their scale|bias words are 16 contiguous bytes of the
+// group's 256-byte chunk.  Loads are issued in the order they are consumed
+// (x, scale|bias, then codes row by row) so the arithmetic starts as data
+// lands.  Rows n0..n0+OUTS-1 with n0 a multiple of 4.
+template <int NV, int MODE>
+__global__ __launch_bounds__(64) void qmv64_tiled_kernel(QmvArgs a) {
   constexpr int OUTS = MODE == 1 ? 4 : 8;
+  constexpr int NQ = 8 / 4;  // 16-byte scale|bias loads per wave-slot of four rows
   const int lane = threadIdx.x;
   const int64_t nblk = (a.n_out + OUTS - 1) / OUTS;
   const int64_t r = blockIdx.x / nblk;
@@ -205,41 +323,55 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   int e = a.experts ? a.experts[r] : 0;
   e = min(max(e, 0), a.num_experts - 1);
   const int64_t xr = a.x_rows ? (int64_t)a.x_rows[r] : r / a.x_div;
-  const int K = a.K;
-  const int G = K / a.group_size;
-  const int64_t KW = K / 8;
-  const int64_t ebase = (int64_t)e * a.n_w;
+  const int G = a.K / 64;
+  const int NC = a.n_w / 64;
+  const int h = lane & 1;
 
-  uint4 wv[8][NV];
-  float sv[8][NV], bv[8][NV];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int oq = MODE == 1 ? (q & 3) : q;
-    const int n = min(n0 + oq, a.n_out - 1);
-    const int64_t row = ebase + n + ((MODE == 1 && q >= 4) ? a.n_out : 0);
-    const uint4* p = reinterpret_cast<const uint4*>(a.w + row * KW) + lane;
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      wv[q][v] = load_nt(p + v * 64);
-      const int g = (v * 2048 + lane * 32) / a.group_size;
-      sv[q][v] = bf16_to_f32(a.s[row * G + g]);
-      bv[q][v] = bf16_to_f32(a.b[row * G + g]);
-    }
-  }
   const uint16_t* xrow = a.x + xr * a.x_stride;
   XChunk xc[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) load_x_chunk(xrow + v * 2048 + lane * 32, xc[v]);
+
+  // the two row quads: MODE 1 gate rows n0.. and up rows n_out + n0..; MODE 0 rows n0.. and n0 + 4..
+  int quad_row[NQ];
+  quad_row[0] = n0;
+  quad_row[1] = MODE == 1 ? a.n_out + n0 : n0 + 4;
+  uint4 sbv[NQ][NV];
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int n = min(quad_row[u], a.n_w - 4);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int g = v * 32 + (lane >> 1);
+      const int64_t chunk = ((int64_t)e * NC + n / 64) * G + g;
+      sbv[u][v] = *reinterpret_cast<const uint4*>(a.sb + chunk * 64 + (n & 63));
+    }
+  }
+  uint4 wv[8][NV];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int n = min(quad_row[q >> 2], a.n_w - 4) + (q & 3);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int g = v * 32 + (lane >> 1);
+      const int64_t unit = ((((int64_t)e * NC + n / 64) * G + g) * 2 + ((n & 63) >> 5)) * 2 + h;
+      wv[q][v] = load_nt(reinterpret_cast<const uint4*>(a.w) + unit * 32 + (n & 31));
+    }
+  }
   float part[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     part[q] = 0.f;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) part[q] += affine_chunk(dot_chunk(wv[q][v], xc[v]), xc[v].sum, sv[q][v], bv[q][v]);
+    for (int v = 0; v < NV; ++v) {
+      const uint4 sq = sbv[q >> 2][v];
+      const uint32_t word = (q & 3) == 0 ? sq.x : (q & 3) == 1 ? sq.y : (q & 3) == 2 ? sq.z : sq.w;
+      part[q] += affine_chunk(dot_chunk(wv[q][v], xc[v]), xc[v].sum, __uint_as_float(word << 16),
+                              __uint_as_float(word & 0xFFFF0000u));
+    }
   }
   const float t = reduce8(part, lane);  // lanes 8q..: row q
   if (MODE == 1) {
-    // gate q sits in lanes 8q (q < 4), up q in lanes 8q + 32
     auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
     const float up = as_f(sw[1]);
     const int q = lane >> 3;
@@ -325,6 +457,8 @@ __global__ __launch_bounds__(1024) void down_wsum_kernel(DownArgs a) {
 
 // Pick lanes-per-row and chunks-per-lane for a reduction length K.
 bool pick_split(int64_t K, int* lpr, int* nv) {
+  *lpr = 0;
+  *nv = 0;
   if (K <= 0 || K % 32) return false;
   const int64_t chunks = K / 32;
   for (int L : {16, 8, 4}) {
@@ -339,17 +473,21 @@ bool pick_split(int64_t K, int* lpr, int* nv) {
 
 template <int MODE>
 int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st) {
-  if (a.K % 2048 == 0 && a.K / 2048 <= 4) {
-    constexpr int outs = MODE == 1 ? 4 : 8;
+  // qmv64 reads scales and biases 16 bytes at a time: G % 8 == 0 and aligned arrays
+  const bool sb_ok = (a.K / a.group_size) % 8 == 0 && qmoe::aligned16(a.s) && qmoe::aligned16(a.b);
+  if (a.K % 2048 == 0 && a.K / 2048 <= 4 && (sb_ok || lpr == 0)) {
+    if (!sb_ok) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "scales and biases must be 16-byte aligned");
+    constexpr int RG = QMOE_QMV_RG;
+    constexpr int outs = MODE == 1 ? RG : 2 * RG;
     const int64_t blocks = a.n_pairs * ((a.n_out + outs - 1) / outs);
     if (blocks <= 0) return QMOE_OK;
     if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
     dim3 grid((unsigned)blocks), block(64);
     switch (a.K / 2048) {
-      case 1: qmv64_kernel<1, MODE><<<grid, block, 0, st>>>(a); break;
-      case 2: qmv64_kernel<2, MODE><<<grid, block, 0, st>>>(a); break;
-      case 3: qmv64_kernel<3, MODE><<<grid, block, 0, st>>>(a); break;
-      default: qmv64_kernel<4, MODE><<<grid, block, 0, st>>>(a); break;
+      case 1: qmv64_kernel<1, MODE, RG><<<grid, block, 0, st>>>(a); break;
+      case 2: qmv64_kernel<2, MODE, RG><<<grid, block, 0, st>>>(a); break;
+      case 3: qmv64_kernel<3, MODE, RG><<<grid, block, 0, st>>>(a); break;
+      default: qmv64_kernel<4, MODE, RG><<<grid, block, 0, st>>>(a); break;
     }
     return qmoe::launch_status("qmv64_kernel");
   }
@@ -369,13 +507,44 @@ int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st) {
   return qmoe::fail(QMOE_ERR_UNSUPPORTED, "no qmv kernel for lpr=%d nv=%d", lpr, nv);
 }
 
+template <int MODE>
+int launch_qmv_tiled(const QmvArgs& a, hipStream_t st) {
+  constexpr int outs = MODE == 1 ? 4 : 8;
+  const int64_t blocks = a.n_pairs * ((a.n_out + outs - 1) / outs);
+  if (blocks <= 0) return QMOE_OK;
+  if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
+  dim3 grid((unsigned)blocks), block(64);
+  switch (a.K / 2048) {
+    case 1: qmv64_tiled_kernel<1, MODE><<<grid, block, 0, st>>>(a); break;
+    case 2: qmv64_tiled_kernel<2, MODE><<<grid, block, 0, st>>>(a); break;
+    case 3: qmv64_tiled_kernel<3, MODE><<<grid, block, 0, st>>>(a); break;
+    default: qmv64_tiled_kernel<4, MODE><<<grid, block, 0, st>>>(a); break;
+  }
+  return qmoe::launch_status("qmv64_tiled_kernel");
+}
+
+int check_tiled(int64_t K, int64_t rows_per_expert, const void* x, const void* wp, const void* sb) {
+  if (K % 2048 || K / 2048 > 4)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: the tile-layout GEMV takes K = 2048 * n, n <= 4", (long long)K);
+  if (rows_per_expert % 64)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "%lld weight rows per expert: must be a multiple of 64",
+                      (long long)rows_per_expert);
+  if (rows_per_expert > 0x3FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "too many rows");
+  if (!qmoe::aligned16(x) || !qmoe::aligned16(wp) || !qmoe::aligned16(sb))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x, wp and sb must be 16-byte aligned");
+  return QMOE_OK;
+}
+
 int check_common(int64_t K, int group_size, int bits, int* lpr, int* nv) {
   if (bits != 4) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "bits=%d: only 4-bit codes have a kernel", bits);
   if (group_size != 32 && group_size != 64 && group_size != 128)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "group_size=%d: kernels take 32, 64 or 128", group_size);
   if (K % group_size) return qmoe::fail(QMOE_ERR_INVALID, "K=%lld not a multiple of group_size", (long long)K);
-  if (!pick_split(K, lpr, nv))
-    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: needs K = 32*L*n, L in {4,8,16}, n <= 8", (long long)K);
+  // K = 2048*n (n <= 4) always has the qmv64 kernel; other K need a lane split
+  const bool qmv64_ok = K % 2048 == 0 && K / 2048 <= 4;
+  if (!pick_split(K, lpr, nv) && !qmv64_ok)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: needs K = 32*L*n, L in {4,8,16}, n <= 8, or 2048*n, n <= 4",
+                      (long long)K);
   return QMOE_OK;
 }
 
@@ -444,6 +613,7 @@ extern "C" int qmoe_moe_down_wsum(const uint16_t* h, const int32_t* idx, const f
   int lpr, nv;
   int rc = check_common(I, group_size, bits, &lpr, &nv);
   if (rc) return rc;
+  if (lpr == 0) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "I=%lld: no lane split for the fused down kernel", (long long)I);
   if (!qmoe::aligned16(h) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "h and w must be 16-byte aligned");
   if (D > 0x3FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "D too large");
   DownArgs a{h, idx, scores, (int)T, (int)top_k, (int)I, group_size, w, scales, biases,
@@ -459,4 +629,31 @@ extern "C" int qmoe_moe_down_wsum(const uint16_t* h, const int32_t* idx, const f
 #undef DW_NV
 #undef DW_CASE
   return qmoe::fail(QMOE_ERR_UNSUPPORTED, "no down kernel for lpr=%d nv=%d", lpr, nv);
+}
+
+extern "C" int qmoe_gather_qmv_tiles(const uint16_t* x, const int32_t* x_rows, const int32_t* experts,
+                                     int64_t n_rows, int64_t K, const uint32_t* wp, const uint32_t* sb,
+                                     int32_t num_experts, int64_t N, uint16_t* out, void* stream) {
+  if (n_rows < 0 || K <= 0 || N <= 0 || num_experts <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (n_rows == 0) return QMOE_OK;
+  if (!x || !wp || !sb || !out) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  const int rc = check_tiled(K, N, x, wp, sb);
+  if (rc) return rc;
+  QmvArgs a{x, K, x_rows, 1, experts, n_rows, (int)K, 64, wp, nullptr, nullptr, num_experts, (int)N, (int)N,
+            out, sb};
+  return launch_qmv_tiled<0>(a, qmoe::as_stream(stream));
+}
+
+extern "C" int qmoe_moe_gate_up_swiglu_tiles(const uint16_t* x, const int32_t* idx, int64_t T, int64_t top_k,
+                                             int64_t K, const uint32_t* wp, const uint32_t* sb,
+                                             int32_t num_experts, int64_t I, uint16_t* h, void* stream) {
+  if (T < 0 || top_k <= 0 || I <= 0 || num_experts <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (T == 0) return QMOE_OK;
+  if (!x || !idx || !wp || !sb || !h) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (I % 4) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "I=%lld: must be a multiple of 4", (long long)I);
+  const int rc = check_tiled(K, 2 * I, x, wp, sb);
+  if (rc) return rc;
+  QmvArgs a{x, K, nullptr, top_k, idx, T * top_k, (int)K, 64, wp, nullptr, nullptr, num_experts, (int)I,
+            (int)(2 * I), h, sb};
+  return launch_qmv_tiled<1>(a, qmoe::as_stream(stream));
 }

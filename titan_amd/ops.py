@@ -311,6 +311,37 @@ def gather_qmm_sorted_tiles(x: torch.Tensor, tw: TileWeights, tiles: TileTable,
     return out
 
 
+def gather_qmv_tiles(x: torch.Tensor, x_rows: torch.Tensor | None, experts: torch.Tensor,
+                     tw: TileWeights) -> torch.Tensor:
+    """:func:`gather_qmv` over tile-layout weights: out[r] = x[x_rows[r]] . W[experts[r]]^T."""
+    x = _bf16(x, "x")
+    K = x.shape[-1]
+    if K != tw.K:
+        raise ValueError(f"x has K={K}, the weights K={tw.K}")
+    ex = _i32(experts.reshape(-1), "experts", x.device)
+    xr = None if x_rows is None else _i32(x_rows.reshape(-1), "x_rows", x.device)
+    n = ex.numel()
+    out = torch.empty(n, tw.N, dtype=torch.bfloat16, device=x.device)
+    _lib.call("qmoe_gather_qmv_tiles", x.data_ptr(), _ptr(xr), ex.data_ptr(), n, K, tw.wp.data_ptr(),
+              tw.sb.data_ptr(), tw.num_experts, tw.N, out.data_ptr(), _stream(x))
+    return out
+
+
+def gate_up_silu_tiles(x: torch.Tensor, tw: TileWeights, idx: torch.Tensor) -> torch.Tensor:
+    """:func:`gate_up_silu` over tile-layout fused gate_up weights [E, 2I, K]."""
+    x = _bf16(x, "x")
+    T, K = x.shape
+    if K != tw.K:
+        raise ValueError(f"x has K={K}, the weights K={tw.K}")
+    idx = _i32(idx, "idx", x.device)
+    k = idx.shape[-1]
+    I = tw.N // 2
+    h = torch.empty(T, k, I, dtype=torch.bfloat16, device=x.device)
+    _lib.call("qmoe_moe_gate_up_swiglu_tiles", x.data_ptr(), idx.data_ptr(), T, k, K, tw.wp.data_ptr(),
+              tw.sb.data_ptr(), tw.num_experts, I, h.data_ptr(), _stream(x))
+    return h
+
+
 def gemm_supported(K: int, N: int, group_size: int, bits: int) -> bool:
     return bits == 4 and group_size == 64 and K % 128 == 0 and N % 256 == 0
 
@@ -500,7 +531,7 @@ def gather_qmm_int8_sorted(xi: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, 
 
 __all__ = [
     "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "TileWeights", "Routing", "build_tiles", "route",
-    "repack_tiles", "gather_qmm_sorted_tiles",
+    "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmv_tiles", "gate_up_silu_tiles",
     "max_tiles", "tile_rows", "unpack", "dequantize", "gather_qmv", "gather_qmm_sorted", "gather_qmm",
     "gemm_supported", "quantized_matmul", "gate_up_silu", "down_wsum", "moe_weighted_sum",
     "quantize_act_int8", "gather_qmm_int8_sorted",
