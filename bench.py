@@ -143,7 +143,7 @@ def calibration_copy(dev, mib=CALIBRATION_MIB, reps=5):
 # `--traffic` measures them live (rocprofv3 children started before this
 # process touches the GPU); otherwise the committed summary supplies them.
 
-TRAFFIC_KERNEL = "qmv64_kernel<1, 1, 2>"
+TRAFFIC_KERNEL = "qmv64_kernel<1, 1, 4>"
 TRAFFIC_PROFILE = ROOT / "profiles" / "qmv64_decode_gate_up.traffic.txt"
 
 
@@ -313,7 +313,7 @@ def setup_cfg1(args, dev):
 
     return wl, [mk_mlx(i) for i in range(args.steps)], {
         "bytes": synth.algorithmic_bytes(1), "flops": synth.algorithmic_flops(1), "bound": "hbm",
-        "kernel": "qmv64_kernel<1,1,2>", "sets": len(sets),
+        "kernel": "qmv64_kernel<1,1,4>", "sets": len(sets),
         "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(args.steps)]),
         "workload": "decode gate_up gather_qmm + SwiGLU: 1 token, H=2048, E=256, top_k=10, "
                     "W [256,1024,2048] int4 g64 bf16 scale/bias -> h [10,512]"}
@@ -386,7 +386,7 @@ def setup_cfg2(args, dev):
     bytes_ = int(mean_distinct * 2048 * row_bytes + 8 * 10 * 512 * 2 + 8 * 2048 * 2 + 8 * 10 * 4)
     return wl, [mk(i) for i in range(args.steps)], {
         "bytes": bytes_, "flops": synth.algorithmic_flops(2, wl), "bound": "hbm",
-        "kernel": "down_wsum_kernel<1,16>", "sets": len(sets), "mean_distinct_experts": mean_distinct,
+        "kernel": "down512_kernel<8>", "sets": len(sets), "mean_distinct_experts": mean_distinct,
         "workload": "decode down + top-10 weighted sum: 8 tokens, I=512, D=2048, E=256, "
                     "W [256,2048,512] int4 g64 -> y [8,2048]"}
 

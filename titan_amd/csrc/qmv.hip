@@ -22,10 +22,18 @@ namespace {
 
 constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
 
-// Rows per row group of the 2048-chunk GEMV (see qmv64_kernel): 2 gives each
-// wave two gate/up pairs, twice as many waves as 4.
-#ifndef QMOE_QMV_RG
-#define QMOE_QMV_RG 2
+// Rows per row group of the 2048-chunk GEMV (see qmv64_kernel).  The fused
+// gate_up form takes four gate/up pairs per wave (1280 waves at top-10 of
+// I = 512); the plain form two groups of two rows (1024 waves at N = 4096).
+#ifndef QMOE_QMV_RG_GU
+#define QMOE_QMV_RG_GU 4
+#endif
+#ifndef QMOE_QMV_RG_DENSE
+#define QMOE_QMV_RG_DENSE 2
+#endif
+// Rows per wave of the I = 512 fused down kernel (a multiple of 4).
+#ifndef QMOE_DOWN_ROWS
+#define QMOE_DOWN_ROWS 8
 #endif
 
 // x pairs laid out to match the nibble pairs of one 32-bit code word:
@@ -51,19 +59,53 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ src, X
   c.sum = s;
 }
 
-// sum over the chunk of x*(128 + q)
-__device__ __forceinline__ float dot_chunk(const uint4& w, const XChunk& c) {
+// (a & m) | c in one v_and_or_b32.  A gfx950 VOP3 instruction encodes no
+// 32-bit literal and reads at most one SGPR, so the mask rides in an SGPR and
+// the bf16 magic in a VGPR (`magic_vgpr()`); left to itself the compiler
+// emits a v_and_b32 and a v_or_b32 with literals, 16 extra VALU ops per chunk.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t d;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(m), "v"(c));
+  return d;
+}
+// kMagic held in a VGPR for and_or; the empty asm keeps it out of constant folding.
+__device__ __forceinline__ uint32_t magic_vgpr() {
+  uint32_t v = kMagic;
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// sum over the chunk of x*(128 + q): 4 and_or + 3 shifts + 4 v_dot2 per word
+__device__ __forceinline__ float dot_chunk(const uint4& w, const XChunk& c, uint32_t mv) {
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t m = 0x000F000Fu;
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t v = ws[j];
-    acc = dot2_bf16((v & 0x000F000Fu) | kMagic, c.p[4 * j + 0], acc);
-    acc = dot2_bf16(((v >> 4) & 0x000F000Fu) | kMagic, c.p[4 * j + 1], acc);
-    acc = dot2_bf16(((v >> 8) & 0x000F000Fu) | kMagic, c.p[4 * j + 2], acc);
-    acc = dot2_bf16(((v >> 12) & 0x000F000Fu) | kMagic, c.p[4 * j + 3], acc);
+    acc = dot2_bf16(and_or(v, m, mv), c.p[4 * j + 0], acc);
+    acc = dot2_bf16(and_or(v >> 4, m, mv), c.p[4 * j + 1], acc);
+    acc = dot2_bf16(and_or(v >> 8, m, mv), c.p[4 * j + 2], acc);
+    acc = dot2_bf16(and_or(v >> 12, m, mv), c.p[4 * j + 3], acc);
   }
   return acc;
+}
+
+// n / d for a divisor fixed at launch and n < 2^31: q = (umulhi(n, m) + n) >> s
+// with s = ceil(log2 d), m = ceil(2^(32+s) / d) - 2^32 (round-up reciprocal;
+// exact because m*d - 2^(32+s) < d <= 2^s).  Replaces 64-bit divisions that
+// the compiler expands into ~40 dependent scalar instructions at kernel entry.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  const uint64_t m = ((1ull << (32 + s)) + d - 1) / d - (1ull << 32);
+  return {d, (uint32_t)m, s};
+}
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
+  return (uint32_t)(((uint64_t)__umulhi(n, f.m) + n) >> f.s);
 }
 
 __device__ __forceinline__ float affine_chunk(float dq, float xsum, float s, float b) {
@@ -87,6 +129,8 @@ struct QmvArgs {
   int n_w;    // weight rows per expert (N, or 2I)
   uint16_t* out;
   const uint32_t* sb;  // tile layout: scale|bias words (w then holds the tile-layout codes)
+  FastDiv blk_div;     // qmv64: blocks per pair
+  FastDiv x_divf;      // qmv64: x_div
 };
 
 // MODE 0: out[r, n] = x_row . W[e][n]
@@ -138,11 +182,12 @@ __global__ __launch_bounds__(64) void qmv_kernel(QmvArgs a) {
 #pragma unroll
   for (int v = 0; v < NV; ++v) load_x_chunk(xrow + v * 32 * LPR + l * 32, xc[v]);
 
+  const uint32_t mv = magic_vgpr();
   float accg = 0.f, accu = 0.f;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    accg += affine_chunk(dot_chunk(wg[v], xc[v]), xc[v].sum, sg[v], bg[v]);
-    if (MODE == 1) accu += affine_chunk(dot_chunk(wu[v], xc[v]), xc[v].sum, su[v], bu[v]);
+    accg += affine_chunk(dot_chunk(wg[v], xc[v], mv), xc[v].sum, sg[v], bg[v]);
+    if (MODE == 1) accu += affine_chunk(dot_chunk(wu[v], xc[v], mv), xc[v].sum, su[v], bu[v]);
   }
   accg = group_sum<LPR>(accg);
   if (MODE == 1) accu = group_sum<LPR>(accu);
@@ -208,31 +253,33 @@ __device__ __forceinline__ uint4 load_nt(const uint4* p) {
 // Scales and biases of the wave's rows -- four segments [array][group][RG rows][G]
 // bf16 taken from the MLX arrays, RG*G/2 16-byte units -- are fetched with
 // one load per lane and unit, staged once in LDS, and read back per lane for
-// its own group.  Loads are issued in the order they are consumed: x, the
-// scales and biases, then the codes row by row; x goes first because it does
-// not wait for the expert id.
-template <int NV, int MODE, int RG>
+// its own group.  The kernel's critical path is three dependent memory round
+// trips (kernel arguments, the expert id, the weights), so the expert id is
+// requested first, x next (it does not wait for the id), then the scales and
+// biases and the codes row by row, in the order they are consumed.
+template <int NV, int MODE, int RG, int GS, bool GATHER, bool XROWS>
 __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   constexpr int OUTS = MODE == 1 ? RG : 2 * RG;
-  constexpr int kMaxUnits = (RG * NV + 1) / 2;  // units per lane at group size 32 (G = 64*NV)
-  __shared__ __attribute__((aligned(16))) uint16_t sbl[4 * RG * 64 * NV];  // [seg][row][G], G <= 64*NV
+  constexpr int G = 2048 * NV / GS;     // groups per row
+  constexpr int UPR = G / 8;            // 16-byte scale units per row
+  constexpr int UNITS = 4 * RG * UPR;   // [array][row group][RG rows][UPR]
+  constexpr int UPL = (UNITS + 63) / 64;
+  __shared__ __attribute__((aligned(16))) uint16_t sbl[UNITS * 8];
   const int lane = threadIdx.x;
-  const int64_t nblk = (a.n_out + OUTS - 1) / OUTS;
-  const int64_t r = blockIdx.x / nblk;
-  if (r >= a.n_pairs) return;
-  const int n0 = (int)(blockIdx.x % nblk) * OUTS;
-  const int64_t xr = a.x_rows ? (int64_t)a.x_rows[r] : r / a.x_div;
-  const uint16_t* xrow = a.x + xr * a.x_stride;
-  XChunk xc[NV];
+  const uint32_t bid = blockIdx.x;
+  const uint32_t r = fast_div(bid, a.blk_div);
+  const int n0 = (int)(bid - r * a.blk_div.d) * OUTS;
+  int e = GATHER ? a.experts[r] : 0;
+  const uint32_t xr = XROWS ? (uint32_t)a.x_rows[r] : fast_div(r, a.x_divf);
+  const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
+  uint4 xa[NV][4];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) load_x_chunk(xrow + v * 2048 + lane * 32, xc[v]);
-  __builtin_amdgcn_sched_barrier(0);
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q];
 
-  int e = a.experts ? a.experts[r] : 0;
   e = min(max(e, 0), a.num_experts - 1);
-  const int K = a.K;
-  const int G = K / a.group_size;
-  const int64_t KW = K / 8;
+  constexpr int64_t KW = 2048 * NV / 8;
   const int64_t ebase = (int64_t)e * a.n_w;
   const int grp1 = MODE == 1 ? a.n_out + n0 : n0 + RG;
   // row of slot (group g, row i), clamped into the expert (slots past n_out are computed, not stored)
@@ -242,19 +289,16 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
     return ebase + min(n, lim);
   };
 
-  const int upr = G / 8;         // 16-byte units per row
-  const int units = 4 * RG * upr;
-  // every lane loads kMaxUnits units (a clamped index repeats the last one) so the
-  // array stays in registers; only the LDS store below is predicated
-  i32x4_t sbv[kMaxUnits];
+  i32x4_t sbv[UPL];
 #pragma unroll
-  for (int j = 0; j < kMaxUnits; ++j) {
-    const int u = min(lane + 64 * j, units - 1);
-    const int seg = u / (RG * upr), rem = u % (RG * upr);
-    const uint16_t* base = (seg >> 1) ? a.b : a.s;
-    sbv[j] = *reinterpret_cast<const i32x4_t*>(base + row_of(seg & 1, rem / upr) * G + (rem % upr) * 8);
+  for (int j = 0; j < UPL; ++j) {
+    const int u = lane + 64 * j;
+    if (UNITS % 64 == 0 || u < UNITS) {
+      const int seg = u / (RG * UPR), rem = u % (RG * UPR);
+      const uint16_t* base = (seg >> 1) ? a.b : a.s;
+      sbv[j] = *reinterpret_cast<const i32x4_t*>(base + row_of(seg & 1, rem / UPR) * G + (rem % UPR) * 8);
+    }
   }
-  __builtin_amdgcn_sched_barrier(0);
   uint4 wv[2][RG][NV];
 #pragma unroll
   for (int g = 0; g < 2; ++g)
@@ -264,14 +308,30 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
 #pragma unroll
       for (int v = 0; v < NV; ++v) wv[g][i][v] = load_nt(p + v * 64);
     }
-  __builtin_amdgcn_sched_barrier(0);
+  XChunk xc[NV];
 #pragma unroll
-  for (int j = 0; j < kMaxUnits; ++j) {
+  for (int v = 0; v < NV; ++v) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 t = xa[v][q];
+      xc[v].p[4 * q + 0] = (t.x & 0xFFFFu) | (t.z << 16);
+      xc[v].p[4 * q + 1] = (t.x >> 16) | (t.z & 0xFFFF0000u);
+      xc[v].p[4 * q + 2] = (t.y & 0xFFFFu) | (t.w << 16);
+      xc[v].p[4 * q + 3] = (t.y >> 16) | (t.w & 0xFFFF0000u);
+      s += ((bf16lo(t.x) + bf16hi(t.x)) + (bf16lo(t.y) + bf16hi(t.y))) +
+           ((bf16lo(t.z) + bf16hi(t.z)) + (bf16lo(t.w) + bf16hi(t.w)));
+    }
+    xc[v].sum = s;
+  }
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
     const int u = lane + 64 * j;
-    if (u < units) *reinterpret_cast<i32x4_t*>(sbl + u * 8) = sbv[j];
+    if (UNITS % 64 == 0 || u < UNITS) *reinterpret_cast<i32x4_t*>(sbl + u * 8) = sbv[j];
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the staged words are visible to the wave
   __builtin_amdgcn_wave_barrier();
+  const uint32_t mv = magic_vgpr();
   float part[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) part[q] = 0.f;
@@ -282,10 +342,10 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
       float acc = 0.f;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        const int gi = (v * 2048 + lane * 32) / a.group_size;
+        const int gi = (v * 2048 + lane * 32) / GS;
         const float sv = bf16_to_f32(sbl[((0 * 2 + g) * RG + i) * G + gi]);
         const float bv = bf16_to_f32(sbl[((1 * 2 + g) * RG + i) * G + gi]);
-        acc += affine_chunk(dot_chunk(wv[g][i][v], xc[v]), xc[v].sum, sv, bv);
+        acc += affine_chunk(dot_chunk(wv[g][i][v], xc[v], mv), xc[v].sum, sv, bv);
       }
       part[4 * g + i] = acc;
     }
@@ -296,11 +356,11 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
     auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
     const float up = as_f(sw[1]);
     if (lane < 32 && (lane & 7) == 0 && q < RG && n0 + q < a.n_out)
-      a.out[r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t / (1.0f + expf(-t)) * up);
+      a.out[(int64_t)r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t / (1.0f + expf(-t)) * up);
   } else {
     const int g = q >> 2, i = q & 3;
     const int n = (g == 0 ? n0 : grp1) + i;
-    if ((lane & 7) == 0 && i < RG && n < a.n_out) a.out[r * a.n_out + n] = (uint16_t)f32_to_bf16(t);
+    if ((lane & 7) == 0 && i < RG && n < a.n_out) a.out[(int64_t)r * a.n_out + n] = (uint16_t)f32_to_bf16(t);
   }
 }
 
@@ -358,6 +418,7 @@ __global__ __launch_bounds__(64) void qmv64_tiled_kernel(QmvArgs a) {
       wv[q][v] = load_nt(reinterpret_cast<const uint4*>(a.w) + unit * 32 + (n & 31));
     }
   }
+  const uint32_t mv = magic_vgpr();
   float part[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
@@ -366,7 +427,7 @@ __global__ __launch_bounds__(64) void qmv64_tiled_kernel(QmvArgs a) {
     for (int v = 0; v < NV; ++v) {
       const uint4 sq = sbv[q >> 2][v];
       const uint32_t word = (q & 3) == 0 ? sq.x : (q & 3) == 1 ? sq.y : (q & 3) == 2 ? sq.z : sq.w;
-      part[q] += affine_chunk(dot_chunk(wv[q][v], xc[v]), xc[v].sum, __uint_as_float(word << 16),
+      part[q] += affine_chunk(dot_chunk(wv[q][v], xc[v], mv), xc[v].sum, __uint_as_float(word << 16),
                               __uint_as_float(word & 0xFFFF0000u));
     }
   }
@@ -414,6 +475,7 @@ __global__ __launch_bounds__(1024) void down_wsum_kernel(DownArgs a) {
   const int I = a.I;
   const int G = I / a.group_size;
   const int64_t KW = I / 8;
+  const uint32_t mv = magic_vgpr();
   float acc = 0.f;
   for (int j0 = 0; j0 < a.k; j0 += kJB) {
     uint4 wv[kJB][NV];
@@ -446,13 +508,132 @@ __global__ __launch_bounds__(1024) void down_wsum_kernel(DownArgs a) {
       for (int v = 0; v < NV; ++v) {
         XChunk hc;
         load_x_chunk(hrow + v * 32 * LPR + l * 32, hc);
-        part += affine_chunk(dot_chunk(wv[jj][v], hc), hc.sum, sv[jj][v], bv[jj][v]);
+        part += affine_chunk(dot_chunk(wv[jj][v], hc, mv), hc.sum, sv[jj][v], bv[jj][v]);
       }
       acc += sc[jj] * part;
     }
   }
   acc = group_sum<LPR>(acc);
   if (l == 0 && valid) a.y[(int64_t)t * a.D + d] = (uint16_t)f32_to_bf16(acc);
+}
+
+// Fused down + weighted sum for I = 512 (one 32-code chunk per lane and row).
+// A block holds W waves of one token t; wave w covers rows
+// d0 = (blockIdx.x*W + w)*R .. d0 + R - 1 of every expert of that token, lane
+// (rg = lane/16, l = lane%16) owning chunk l of rows d0 + 4i + rg (i < R/4),
+// so each 16-byte load instruction reads four consecutive 256-byte rows.
+//  * Loads of all of the token's (up to kDownMaxK) experts are issued before
+//    any arithmetic: the codes and scales are one dependent round trip after
+//    the expert ids, with nothing batched behind them.
+//  * The token's k rows of h are turned into x pairs and 32-element sums once
+//    per block, in LDS ([expert][pair quad][chunk] 16-byte units, read
+//    conflict-free), instead of once per wave and expert.
+//  * The router score is folded into the per-lane partial; one 16-lane
+//    reduction per row ends the weighted sum (fused_kernels.py:93-169).
+// Tokens that share an expert read its rows from L2 or the Infinity Cache.
+constexpr int kDownMaxK = 12;
+constexpr int kDownWaves = 4;  // waves per block
+
+template <int R>
+__global__ __launch_bounds__(64 * kDownWaves) void down512_kernel(DownArgs a) {
+  constexpr int NI = R / 4;
+  __shared__ uint4 hp[kDownMaxK][5][16];  // pair words 4q..4q+3 in [j][q][l]; [j][4][l].x = chunk sum
+  const int t = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  constexpr int W = kDownWaves;
+  const int rg = lane >> 4, l = lane & 15;
+  const int d0 = (blockIdx.x * W + w) * R;
+  const int k = a.k, D = a.D;
+  const int G = 512 / a.group_size;
+  const int gi = (l * 32) / a.group_size;
+  const int64_t pbase = (int64_t)t * k;
+
+  // h chunks this thread formats (k*16 items over the block)
+  const int nitems = k * 16;
+  constexpr int kItemsMax = (kDownMaxK * 16 + 64 * W - 1) / (64 * W);
+  uint4 hv[kItemsMax][4];
+#pragma unroll
+  for (int it = 0; it < kItemsMax; ++it) {
+    const int item = threadIdx.x + it * 64 * W;
+    if (item < nitems) {
+      const uint4* src = reinterpret_cast<const uint4*>(a.h + (pbase + item / 16) * 512 + (item % 16) * 32);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hv[it][q] = src[q];
+    }
+  }
+
+  uint4 wq[kDownMaxK][NI];
+  uint16_t sv[kDownMaxK][NI], bv[kDownMaxK][NI];
+  float sc[kDownMaxK];
+#pragma unroll
+  for (int j = 0; j < kDownMaxK; ++j) {
+    if (j < k) {
+      int e = a.idx[pbase + j];
+      e = min(max(e, 0), a.num_experts - 1);
+      sc[j] = a.scores[pbase + j];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int64_t row = (int64_t)e * D + min(d0 + 4 * i + rg, D - 1);
+        wq[j][i] = load_nt(reinterpret_cast<const uint4*>(a.w + row * 64) + l);
+        sv[j][i] = a.s[row * G + gi];
+        bv[j][i] = a.b[row * G + gi];
+      }
+    }
+  }
+
+#pragma unroll
+  for (int it = 0; it < kItemsMax; ++it) {
+    const int item = threadIdx.x + it * 64 * W;
+    if (item < nitems) {
+      const int j = item / 16, c = item % 16;
+      uint32_t p[16];
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = hv[it][q];
+        p[4 * q + 0] = (v.x & 0xFFFFu) | (v.z << 16);
+        p[4 * q + 1] = (v.x >> 16) | (v.z & 0xFFFF0000u);
+        p[4 * q + 2] = (v.y & 0xFFFFu) | (v.w << 16);
+        p[4 * q + 3] = (v.y >> 16) | (v.w & 0xFFFF0000u);
+        s += ((bf16lo(v.x) + bf16hi(v.x)) + (bf16lo(v.y) + bf16hi(v.y))) +
+             ((bf16lo(v.z) + bf16hi(v.z)) + (bf16lo(v.w) + bf16hi(v.w)));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hp[j][q][c] = make_uint4(p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]);
+      hp[j][4][c] = make_uint4(__float_as_uint(s), 0u, 0u, 0u);
+    }
+  }
+  __syncthreads();
+
+  const uint32_t mv = magic_vgpr();
+  float acc[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int j = 0; j < kDownMaxK; ++j) {
+    if (j < k) {
+      XChunk hc;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 u = hp[j][q][l];
+        hc.p[4 * q] = u.x;
+        hc.p[4 * q + 1] = u.y;
+        hc.p[4 * q + 2] = u.z;
+        hc.p[4 * q + 3] = u.w;
+      }
+      hc.sum = __uint_as_float(hp[j][4][l].x);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        acc[i] += sc[j] * affine_chunk(dot_chunk(wq[j][i], hc, mv), hc.sum, bf16_to_f32(sv[j][i]),
+                                       bf16_to_f32(bv[j][i]));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const float v = group_sum<16>(acc[i]);
+    const int d = d0 + 4 * i + rg;
+    if (l == 0 && d < D) a.y[(int64_t)t * D + d] = (uint16_t)f32_to_bf16(v);
+  }
 }
 
 // Pick lanes-per-row and chunks-per-lane for a reduction length K.
@@ -471,25 +652,58 @@ bool pick_split(int64_t K, int* lpr, int* nv) {
   return false;
 }
 
+template <int MODE, int RG, int NV, int GS>
+int launch_qmv64_k(const QmvArgs& a, dim3 grid, hipStream_t st) {
+  if (MODE == 1) {
+    qmv64_kernel<NV, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
+  } else if (!a.experts) {
+    qmv64_kernel<NV, MODE, RG, GS, false, false><<<grid, dim3(64), 0, st>>>(a);
+  } else if (a.x_rows) {
+    qmv64_kernel<NV, MODE, RG, GS, true, true><<<grid, dim3(64), 0, st>>>(a);
+  } else {
+    qmv64_kernel<NV, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
+  }
+  return qmoe::launch_status("qmv64_kernel");
+}
+
+template <int MODE, int RG, int NV>
+int launch_qmv64_nv(const QmvArgs& a, dim3 grid, hipStream_t st) {
+  switch (a.group_size) {
+    case 32: return launch_qmv64_k<MODE, RG, NV, 32>(a, grid, st);
+    case 64: return launch_qmv64_k<MODE, RG, NV, 64>(a, grid, st);
+    default: return launch_qmv64_k<MODE, RG, NV, 128>(a, grid, st);
+  }
+}
+
+template <int MODE, int RG>
+int launch_qmv64(const QmvArgs& a, dim3 grid, hipStream_t st) {
+  switch (a.K / 2048) {
+    case 1: return launch_qmv64_nv<MODE, RG, 1>(a, grid, st);
+    case 2: return launch_qmv64_nv<MODE, RG, 2>(a, grid, st);
+    case 3: return launch_qmv64_nv<MODE, RG, 3>(a, grid, st);
+    default: return launch_qmv64_nv<MODE, RG, 4>(a, grid, st);
+  }
+}
+
 template <int MODE>
 int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st) {
   // qmv64 reads scales and biases 16 bytes at a time: G % 8 == 0 and aligned arrays
   const bool sb_ok = (a.K / a.group_size) % 8 == 0 && qmoe::aligned16(a.s) && qmoe::aligned16(a.b);
   if (a.K % 2048 == 0 && a.K / 2048 <= 4 && (sb_ok || lpr == 0)) {
     if (!sb_ok) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "scales and biases must be 16-byte aligned");
-    constexpr int RG = QMOE_QMV_RG;
+    constexpr int RG = MODE == 1 ? QMOE_QMV_RG_GU : QMOE_QMV_RG_DENSE;
     constexpr int outs = MODE == 1 ? RG : 2 * RG;
-    const int64_t blocks = a.n_pairs * ((a.n_out + outs - 1) / outs);
+    const int64_t nblk = (a.n_out + outs - 1) / outs;
+    const int64_t blocks = a.n_pairs * nblk;
     if (blocks <= 0) return QMOE_OK;
     if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
+    if (!a.x_rows && (a.x_div < 1 || a.x_div > 0x7FFFFFFF))
+      return qmoe::fail(QMOE_ERR_INVALID, "x_div=%lld out of range", (long long)a.x_div);
+    QmvArgs b = a;
+    b.blk_div = make_fastdiv((uint32_t)nblk);
+    b.x_divf = make_fastdiv(a.x_rows ? 1u : (uint32_t)a.x_div);
     dim3 grid((unsigned)blocks), block(64);
-    switch (a.K / 2048) {
-      case 1: qmv64_kernel<1, MODE, RG><<<grid, block, 0, st>>>(a); break;
-      case 2: qmv64_kernel<2, MODE, RG><<<grid, block, 0, st>>>(a); break;
-      case 3: qmv64_kernel<3, MODE, RG><<<grid, block, 0, st>>>(a); break;
-      default: qmv64_kernel<4, MODE, RG><<<grid, block, 0, st>>>(a); break;
-    }
-    return qmoe::launch_status("qmv64_kernel");
+    return launch_qmv64<MODE, RG>(b, grid, st);
   }
   const int gpw = 64 / lpr;
   const int64_t nblk = (a.n_out + gpw - 1) / gpw;
@@ -618,9 +832,18 @@ extern "C" int qmoe_moe_down_wsum(const uint16_t* h, const int32_t* idx, const f
   if (D > 0x3FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "D too large");
   DownArgs a{h, idx, scores, (int)T, (int)top_k, (int)I, group_size, w, scales, biases,
              num_experts, (int)D, y};
+  hipStream_t st = qmoe::as_stream(stream);
+  if (I == 512 && top_k <= kDownMaxK && qmoe::aligned16(h)) {
+    // blocks of kDownWaves waves of one token, R rows per wave
+    constexpr int R = QMOE_DOWN_ROWS;
+    const int64_t waves_per_token = (D + R - 1) / R;
+    dim3 grid2((unsigned)((waves_per_token + kDownWaves - 1) / kDownWaves), (unsigned)T),
+        block2(64 * kDownWaves);
+    down512_kernel<R><<<grid2, block2, 0, st>>>(a);
+    return qmoe::launch_status("down512_kernel");
+  }
   const int gpw = 64 / lpr;
   dim3 grid((unsigned)((D + gpw - 1) / gpw)), block((unsigned)(64 * T));
-  hipStream_t st = qmoe::as_stream(stream);
 #define DW_CASE(NV_, L_) \
   if (nv == NV_ && lpr == L_) { down_wsum_kernel<NV_, L_><<<grid, block, 0, st>>>(a); return qmoe::launch_status("down_wsum_kernel"); }
 #define DW_NV(L_) DW_CASE(1, L_) DW_CASE(2, L_) DW_CASE(3, L_) DW_CASE(4, L_) \
