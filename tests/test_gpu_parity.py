@@ -240,6 +240,55 @@ def test_sorted_gemm_bf16(dev, orc, E, N, K, R, kind):
     assert rep["rel_to_max"] <= 2.0 ** -8
 
 
+@pytest.mark.parametrize("tiled", [False, True])
+def test_sorted_gemm_dequant_bit_exact_one_hot(dev, orc, tiled):
+    """Rows of x are one-hot, so y[r, n] = x[r, k_r] * deq(W)[n, k_r] with a
+    single nonzero product: the GEMM output is the in-kernel dequantised
+    weight itself, which must equal bf16_rne(fmaf(q, s, b)) bit for bit
+    (moe_gather_ws.py:343-344) for every code position of every word."""
+    say(f"sorted GEMM one-hot dequant tiled={tiled}")
+    rng = np.random.default_rng(11)
+    E, N, K = 2, 256, 256
+    w, s, b = synth.quant_weights(rng, (E, N), K)
+    R = 2 * K  # expert 0 and expert 1 each see every k once
+    ids = np.repeat(np.arange(E), K).astype(np.int32)
+    x = np.zeros((R, K), np.float32)
+    x[np.arange(R), np.tile(np.arange(K), E)] = 1.0
+    xb = synth.bf16_bits(x)
+    tiles = ops.build_tiles(i32_t(ids, dev), E)
+    if tiled:
+        tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+        y = ops.gather_qmm_sorted_tiles(bf16_t(xb, dev), tw, tiles)
+    else:
+        y = ops.gather_qmm_sorted(bf16_t(xb, dev), words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
+    got = bits(y).reshape(E, K, N)
+    deq = orc.dequantize_bf16(w, s, b, 64, 4)  # bf16 bits [E, N, K]
+    assert np.array_equal(got, deq.transpose(0, 2, 1))
+
+
+@pytest.mark.parametrize("tiled", [False, True])
+def test_sorted_gemm_every_subtile_count(dev, orc, tiled):
+    """Experts with 1, 33, 65, ... 225, 256 and 300 rows: tiles of every
+    32-row subtile count 1..8, a full tile and a tile boundary inside an
+    expert."""
+    counts = [1, 33, 65, 97, 129, 161, 193, 225, 256, 300, 0, 31]
+    E, N, K = len(counts), 512, 512
+    say(f"sorted GEMM every subtile count tiled={tiled}")
+    rng = np.random.default_rng(5)
+    w, s, b = synth.quant_weights(rng, (E, N), K)
+    ids = np.repeat(np.arange(E), counts).astype(np.int32)
+    R = len(ids)
+    x = synth.bf16_bits(rng.normal(size=(R, K)).astype(np.float32))
+    tiles = ops.build_tiles(i32_t(ids, dev), E)
+    if tiled:
+        tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+        y = ops.gather_qmm_sorted_tiles(bf16_t(x, dev), tw, tiles)
+    else:
+        y = ops.gather_qmm_sorted(bf16_t(x, dev), words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
+    ref, _ = orc.gather_qmm_rows(x, None, ids, w, s, b, deq="bf16")
+    assert_close_bf16(orc, bits(y), ref, what="gemm every subtile count")
+
+
 def test_gather_qmm_sorted_with_lhs_indices(dev, orc):
     """The fused-gather form: x token-major, lhs_indices = order // k."""
     say("gather_qmm sorted with lhs_indices")

@@ -3,33 +3,45 @@
 // Semantics: titan/kernels/moe_gather_ws.py:20-32 -- weights dequantised to
 // bf16 as bf16_rne(fmaf(q, s, b)) (:343-344), bf16 x bf16 products, fp32
 // accumulation.  Work unit: one (tile, column block).  A tile is up to
-// kBM = 128 consecutive sorted rows of one expert (the tile list of the
-// routing step); a column block is 64 * W output columns, one 64-column
-// slice for each of the block's W waves (W = 8 when N is a multiple of 512,
-// else 4).  Wide column blocks matter: the activation rows of a tile are
-// fetched once per column block, and that re-fetch, not arithmetic, is the
-// limit at 256 columns.
+// kBM = 256 consecutive sorted rows of one expert (the tile list of the
+// routing step); a column block is kBN = 256 output columns, one 64-column
+// slice for each of the block's four waves.  Every wave covers all the
+// tile's rows, so each weight element is dequantised once per tile.
+//
+// Register budget: one wave per SIMD, so a wave may hold 512 registers.  Its
+// 256 x 64 output tile is 8 x 2 subtiles of 32 x 32 fp32 (256 accumulator
+// registers, in AGPRs); operands and addresses use the VGPRs.
+//
+// Per 64-wide K group (one quantisation group) a wave
+//   - dequantises its 64 columns' codes in registers (two 16-byte code
+//     chunks per lane: 64 codes), 17 VALU instructions per 8 codes:
+//     the nibbles are masked into the low bits of 16-bit halves, where they
+//     read as fp16 denormals q * 2^-24 (bits 0..3) or q * 2^-20 (bits 4..7);
+//     v_fma_mix_f32 widens them exactly and computes
+//     fma(q * 2^-24, s * 2^24, b) == fmaf(q, s, b) bit for bit (scaling by a
+//     power of two is exact), then v_cvt_pk_bf16_f32 rounds to nearest even;
+//   - runs 4 k-steps x 16 v_mfma_f32_32x32x16_bf16, weights as the A operand
+//     (rows = output columns) and activations as B (columns = token rows), so
+//     each lane ends up owning four consecutive output columns per register
+//     quad and the epilogue stores 8 bytes at a time.
 //
 // Data movement: every operand byte reaches LDS through asynchronous copies
-// (global_load_lds_dwordx4 / _dword, issued from inline assembly so that the
-// copies stay in flight across iterations; the wait counts are explicit).  A
-// ring of kStages stages each holds one 64-wide K group (one quantisation
-// group):
-//   A  the tile's activation rows, gathered through x_rows, 128 x 128 bytes,
-//      16-byte units XOR-swizzled by row (swz) so MFMA operand reads are
-//      bank-conflict free;
-//   B  each wave's 64 columns of packed codes (16 bytes per lane and column
-//      subtile: the lane's own half group);
+// (global_load_lds_dwordx4 / _dword from inline assembly, so the copies stay
+// in flight across iterations with explicit wait counts) into a ring of
+// kStages stages.  A stage holds
+//   A  the tile's activation rows for the group, gathered through x_rows,
+//      256 x 128 bytes, 16-byte units XOR-swizzled by row (swz) so operand
+//      reads are bank-conflict free; only the subtiles the tile has are copied;
+//   B  each wave's 64 columns of packed codes (16 bytes per lane and subtile);
 //   S  the 64 columns' scales and biases.
-// Per group a wave dequantises its own codes in registers into the MFMA B
-// operand (columns are wave-private, so no dequant work is repeated) and runs
-// four k-steps of v_mfma_f32_32x32x16_bf16 per 32 x 32 subtile.  Row subtiles
-// past the tile's valid rows are compiled out (the loop is instantiated per
-// subtile count), so a short tail tile costs only its own MFMAs.
+// Row subtiles past a tile's valid rows are compiled out (the loop is
+// instantiated per subtile count 1..8), so a short tile costs only its own
+// MFMAs and copies.
 //
 // K order inside a group is free as long as A and B agree: lane half h
 // supplies group elements 32h + 8kk .. +7 at k-step kk -- word kk of the
 // lane's 16-byte code chunk and 16-byte unit 4h + kk of the activation row.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -37,28 +49,29 @@
 namespace {
 
 constexpr int kBM = 128;
-constexpr int kABytes = kBM * 128;  // one group of the tile's activation rows: 16 KiB
+constexpr int kMaxSub = kBM / 32;
+constexpr int kWaves = 4;
+constexpr int kBN = 64 * kWaves;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kStages = 3;
+constexpr int kBlocksPerCU = 2;
 
-// Layout and pipeline of one instantiation with W waves per block.  W = 8:
-// 512 columns, a ring of 4 stages of 36 KiB, one block per CU.  W = 4: 256
-// columns, 2 stages of 26 KiB, two blocks per CU.
-template <int W>
+// Stage layout (bytes).  TILED: one scale|bias word per column; MLX layout:
+// a scale pair and a bias pair (two groups) per column.
+template <bool TILED>
 struct Cfg {
-  static constexpr int kWaves = W;
-  static constexpr int kBN = 64 * W;
-  static constexpr int kThreads = 64 * W;
-  static constexpr int kStages = W == 8 ? 4 : 2;
-  static constexpr int kBlocksPerCU = W == 8 ? 1 : 2;
-  // stage layout (bytes)
   static constexpr int kAOff = 0;
+  static constexpr int kABytes = kBM * 128;
   static constexpr int kBOff = kAOff + kABytes;
-  static constexpr int kBBytes = W * 2 * 64 * 16;  // [wave][subtile][lane] x 16 B
+  static constexpr int kBBytes = kWaves * 2 * 64 * 16;  // [wave][subtile][lane] x 16 B
   static constexpr int kSOff = kBOff + kBBytes;
-  static constexpr int kSBytes = W * 2 * 64 * 4;  // [wave][scale|bias][lane] x 4 B
+  static constexpr int kSBytes = kWaves * (TILED ? 1 : 2) * 64 * 4;
   static constexpr int kStageBytes = kSOff + kSBytes;
-  static constexpr int kACopies = kABytes / (W * 1024);  // 16-byte-per-lane copies of A per wave
-  static_assert(kStages * kStageBytes * kBlocksPerCU <= 160 * 1024, "LDS per CU");
-  static_assert(kStages >= 2 && kStages <= 4, "wait_group covers up to two groups in flight");
+  static constexpr int kLdsBytes = kStages * kStageBytes;
+  static_assert(kBlocksPerCU * (kLdsBytes + 4 * 512) <= 160 * 1024, "LDS per CU");
+  // copies per wave and group besides A: two code chunks, one (tiled) or two
+  // (scale pair, bias pair) scale copies
+  static constexpr int kOtherCopies = 2 + (TILED ? 1 : 2);
 };
 
 struct GemmArgs {
@@ -80,30 +93,24 @@ struct GemmArgs {
 };
 
 // Asynchronous 16- and 4-byte copies into LDS: lane i writes
-// lds_base + i * size.  M0 carries the wave's LDS base and is restored.
+// lds_base + i * size.  M0 carries the LDS base (declared clobbered).
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
-  uint32_t saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
+      "global_load_lds_dwordx4 %1, off"
+      :
       : "s"(lds_base), "v"(g)
-      : "memory");
+      : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
-  uint32_t saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dword %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
+      "global_load_lds_dword %1, off"
+      :
       : "s"(lds_base), "v"(g)
-      : "memory");
+      : "memory", "m0");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmem() {
@@ -117,30 +124,12 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// Byte b of v as a float: one v_cvt_f32_ubyte<b>.  Written as assembly
-// because the compiler otherwise folds the preceding nibble mask into a
-// bit-field extract and spends two instructions per code.
-template <int B>
-__device__ __forceinline__ float ubyte(uint32_t v) {
-  float r;
-  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-  else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-  else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-  return r;
-}
-
-// 8 codes of one word -> 8 bf16 (k order 0..7), bf16_rne(fmaf(q, s, b)).
-// lo holds codes 0,2,4,6 in its bytes, hi codes 1,3,5,7.
-__device__ __forceinline__ i32x4_t dequant_word(uint32_t v, float s, float b) {
-  const uint32_t lo = v & 0x0F0F0F0Fu;
-  const uint32_t hi = (v >> 4) & 0x0F0F0F0Fu;
-  i32x4_t r;
-  r[0] = (int)cvt_pk_bf16(__builtin_fmaf(ubyte<0>(lo), s, b), __builtin_fmaf(ubyte<0>(hi), s, b));
-  r[1] = (int)cvt_pk_bf16(__builtin_fmaf(ubyte<1>(lo), s, b), __builtin_fmaf(ubyte<1>(hi), s, b));
-  r[2] = (int)cvt_pk_bf16(__builtin_fmaf(ubyte<2>(lo), s, b), __builtin_fmaf(ubyte<2>(hi), s, b));
-  r[3] = (int)cvt_pk_bf16(__builtin_fmaf(ubyte<3>(lo), s, b), __builtin_fmaf(ubyte<3>(hi), s, b));
-  return r;
+// fma(h, s, b) in fp32 with h the fp16 in the low (HI = false) or high half
+// of v, widened exactly (fp16 denormals included): one v_fma_mix_f32.
+template <bool HI>
+__device__ __forceinline__ float fma_mix(uint32_t v, float s, float b) {
+  const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(HI ? v >> 16 : v));
+  return __builtin_fmaf((float)h, s, b);
 }
 
 // Row swizzle of the 16-byte units of an activation row in LDS: unit u of
@@ -150,133 +139,268 @@ __device__ __forceinline__ i32x4_t dequant_word(uint32_t v, float s, float b) {
 // over the eight rows of each parity among r..r+15).
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-// Copies per wave and group: A, two B, and the scales and biases -- two
-// 4-byte copies (scale pair, bias pair) from the MLX layout, one (the
-// column's scale|bias word) from the tile layout.
-template <int W, bool TILED>
-constexpr int kDmaPerGroup = Cfg<W>::kACopies + 2 + (TILED ? 1 : 2);
-
-template <int W>
+template <bool TILED>
 struct Ctx {
   // per-lane global sources at group 0 (advance per group)
-  const char* a_src[Cfg<W>::kACopies];  // activation 16-byte units, one per A copy
-  const char* b_src[2];  // codes of the lane's column in each subtile
-  const char* s_src;     // MLX layout: scale pair (groups 2j, 2j+1) of column (wave*64 + lane);
-                         // tile layout: scale|bias word of that column
-  const char* z_src;     // MLX layout: bias pair
-  uint32_t lds;          // LDS address of the ring
-  uint32_t a_dst[Cfg<W>::kACopies];  // wave-uniform LDS offsets within a stage
-  uint32_t b_dst[2];
-  uint32_t s_dst, z_dst;
+  const char* a_src[kMaxSub];  // activation 16-byte unit of the lane's row in A copy q
+  const char* b_src[2];        // codes of the lane's column in each subtile
+  const char* s_src;           // MLX layout: scale pair (groups 2j, 2j+1) of column (wave*64 + lane);
+                               // tile layout: scale|bias word of that column
+  const char* z_src;           // MLX layout: bias pair
+  uint32_t lds;                // LDS address of the ring
   int G;
   int wave, lane, l32, h;
 };
 
-template <int W, bool TILED>
-__device__ __forceinline__ void issue_group(const Ctx<W>& c, int g) {
-  using C = Cfg<W>;
-  const uint32_t st = c.lds + (uint32_t)(g % C::kStages) * C::kStageBytes;
-#pragma unroll
-  for (int q = 0; q < C::kACopies; ++q) dma16(c.a_src[q] + (size_t)g * 128, st + c.a_dst[q]);
+// Copy d (0 <= d < MSUB + kOtherCopies) of group g into its ring stage:
+// d < MSUB is activation copy q = d (rows 32q + 8*wave .. +7 of subtile q),
+// then the two code chunks, then the scales and biases.
+template <bool TILED, int MSUB>
+__device__ __forceinline__ void issue_copy(const Ctx<TILED>& c, int g, int d) {
+  using C = Cfg<TILED>;
+  const uint32_t st = c.lds + (uint32_t)(g % kStages) * C::kStageBytes;
+  if (d < MSUB) {
+    dma16(c.a_src[d] + (size_t)g * 128, st + C::kAOff + (uint32_t)(d * kWaves + c.wave) * 1024);
+    return;
+  }
+  const int j = d - MSUB;
+  const uint32_t bdst = st + C::kBOff + (uint32_t)c.wave * 2048;
   if constexpr (TILED) {
     // one 2 KiB code chunk and one 256-byte scale|bias chunk per group
-#pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(c.b_src[j] + (size_t)g * 2048, st + c.b_dst[j]);
-    dma4(c.s_src + (size_t)g * 256, st + c.s_dst);
+    if (j < 2) dma16(c.b_src[j] + (size_t)g * 2048, bdst + j * 1024);
+    else dma4(c.s_src + (size_t)g * 256, st + C::kSOff + c.wave * 256);
   } else {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(c.b_src[j] + (size_t)g * 32, st + c.b_dst[j]);
-    dma4(c.s_src + (size_t)(g >> 1) * 4, st + c.s_dst);
-    dma4(c.z_src + (size_t)(g >> 1) * 4, st + c.z_dst);
+    if (j < 2) dma16(c.b_src[j] + (size_t)g * 32, bdst + j * 1024);
+    else if (j == 2) dma4(c.s_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.wave * 512);
+    else dma4(c.z_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.wave * 512 + 256);
   }
 }
 
-// Wait until this wave's copies of group g have landed: the copies of the
-// groups issued after it (at most kStages - 2, each kDmaPerGroup copies)
-// may stay in flight.
-template <int D>
-__device__ __forceinline__ void wait_group(int ahead) {
-  if (ahead >= 2) wait_vmem<2 * D>();
-  else if (ahead == 1) wait_vmem<D>();
-  else wait_vmem<0>();
+template <bool TILED, int MSUB>
+__device__ __forceinline__ void issue_group(const Ctx<TILED>& c, int g) {
+#pragma unroll
+  for (int d = 0; d < MSUB + Cfg<TILED>::kOtherCopies; ++d) issue_copy<TILED, MSUB>(c, g, d);
 }
 
-template <int W, bool TILED, int MSUB>
-__device__ __forceinline__ void tile_loop(const Ctx<W>& c, const char* smem, f32x16_t (&acc)[4][2]) {
-  using C = Cfg<W>;
-  constexpr int kStages = C::kStages, kAOff = C::kAOff, kBOff = C::kBOff, kSOff = C::kSOff;
+// Operands of one k-step: the wave's two dequantised weight fragments and the
+// MSUB activation fragments.
+template <int MSUB>
+struct Frag {
+  i32x4_t b[2];
+  i32x4_t a[MSUB];
+};
+
+// Per-group state of the weight side: the lane's 8 code words and the raw
+// scale and bias words of its two columns (converted where the first dequant
+// uses them, so the conversion does not wait on LDS ahead of the MFMAs).
+struct WState {
+  uint32_t w[2][4];
+  uint32_t sraw[2], zraw[2];  // words holding column j's scale and bias as bf16 halves
+  int s_sh, z_sh;             // bit offset of the scale / bias half (0 or 16)
+};
+
+template <bool TILED>
+__device__ __forceinline__ WState load_wstate(const Ctx<TILED>& c, const char* st, int g) {
+  using C = Cfg<TILED>;
+  WState ws;
+  const uint4 raw0 = *reinterpret_cast<const uint4*>(st + C::kBOff + c.wave * 2048 + c.lane * 16);
+  const uint4 raw1 = *reinterpret_cast<const uint4*>(st + C::kBOff + c.wave * 2048 + 1024 + c.lane * 16);
+  ws.w[0][0] = raw0.x; ws.w[0][1] = raw0.y; ws.w[0][2] = raw0.z; ws.w[0][3] = raw0.w;
+  ws.w[1][0] = raw1.x; ws.w[1][1] = raw1.y; ws.w[1][2] = raw1.z; ws.w[1][3] = raw1.w;
+  if constexpr (TILED) {
+    // one word per column: scale in the low half, bias in the high half
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.wave * 256);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) ws.sraw[j] = ws.zraw[j] = sw[c.l32 + 32 * j];
+    ws.s_sh = 0;
+    ws.z_sh = 16;
+  } else {
+    // scale pair and bias pair of groups (2m, 2m+1): group g in half g & 1
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.wave * 512);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      ws.sraw[j] = sw[c.l32 + 32 * j];
+      ws.zraw[j] = sw[64 + c.l32 + 32 * j];
+    }
+    ws.s_sh = ws.z_sh = (g & 1) * 16;
+  }
+  return ws;
+}
+
+template <int MSUB>
+__device__ __forceinline__ void read_a(Frag<MSUB>& f, const char* abuf, int kk, int l32, int h) {
+  const int unit = (4 * h + kk) ^ swz(l32);  // swz(32i + l32) == swz(l32)
+#pragma unroll
+  for (int i = 0; i < MSUB; ++i) f.a[i] = *reinterpret_cast<const i32x4_t*>(abuf + (32 * i + l32) * 128 + unit * 16);
+}
+
+// Dword d = q % 4 of the dequantised fragment of code word j = q / 4 at
+// k-step kk: bf16_rne(fmaf(code, s, b)) of the word's codes 2d and 2d + 1,
+// low half first (k order).  The word's codes sit at bits 4t..4t+3; masking keeps two of
+// them in the low bits of the 16-bit halves, where they read as fp16
+// denormals: code 0 | 4 as q * 2^-24 (bits 0..3 of each half), code 1 | 5 as
+// q * 2^-20 (bits 4..7); shifting the word by 8 first gives codes 2 | 6 and
+// 3 | 7.  d & 2 selects the high halves (codes 4..7).
+__device__ __forceinline__ void dequant_piece(i32x4_t (&b)[2], const WState& ws, int kk, int q) {
+  const int j = q >> 2, d = q & 3;
+  const float sc = __uint_as_float((ws.sraw[j] >> ws.s_sh) << 16);
+  const float s24 = sc * 16777216.0f, s20 = sc * 1048576.0f;  // exact
+  const float z = __uint_as_float((ws.zraw[j] >> ws.z_sh) << 16);
+  const uint32_t v = (d & 1) ? ws.w[j][kk] >> 8 : ws.w[j][kk];
+  const uint32_t lo = v & 0x000F000Fu, hi = v & 0x00F000F0u;
+  if (d & 2)
+    b[j][d] = (int)cvt_pk_bf16(fma_mix<true>(lo, s24, z), fma_mix<true>(hi, s20, z));
+  else
+    b[j][d] = (int)cvt_pk_bf16(fma_mix<false>(lo, s24, z), fma_mix<false>(hi, s20, z));
+}
+
+// One k-step: the activation fragments are read and the weight fragment
+// dequantised, then the MFMAs run in MSUB slots of two, slot p carrying the
+// copies d of group cg whose place among the group's 4 * MSUB slots is
+// 4 * kk + p... spread evenly: a scheduling barrier after every slot keeps the
+// copies trickling out between MFMAs instead of stalling the wave in a burst.
+// Latency is hidden by the other block on the CU (two blocks per CU).
+template <bool TILED, int MSUB, bool COPY>
+__device__ __forceinline__ void step(const Ctx<TILED>& c, const WState& ws, const char* abuf, int kk, int cg,
+                                     f32x16_t (&acc)[kMaxSub][2]) {
+  constexpr int D = MSUB + Cfg<TILED>::kOtherCopies;
+  constexpr int kSlots = 4 * MSUB;
+  Frag<MSUB> f;
+  read_a<MSUB>(f, abuf, kk, c.l32, c.h);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) dequant_piece(f.b, ws, kk, q);
+#pragma unroll
+  for (int p = 0; p < MSUB; ++p) {
+    acc[p][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.b[0]),
+                                                        __builtin_bit_cast(bf16x8_t, f.a[p]), acc[p][0], 0, 0, 0);
+    acc[p][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.b[1]),
+                                                        __builtin_bit_cast(bf16x8_t, f.a[p]), acc[p][1], 0, 0, 0);
+    if constexpr (COPY) {
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+        if (d * kSlots / D == kk * MSUB + p) issue_copy<TILED, MSUB>(c, cg, d);
+    }
+  }
+}
+
+// One tile's main loop over the K groups, a ring of kStages stages with the
+// copies of group g + 2 in flight while group g is computed.  Every
+// iteration copies a group (the last group again once the tile is exhausted
+// -- into a stage nobody reads any more), so the loop body has no branches.
+template <bool TILED, int MSUB>
+__device__ __forceinline__ void tile_loop(const Ctx<TILED>& c, const char* smem, f32x16_t (&acc)[kMaxSub][2]) {
+  using C = Cfg<TILED>;
+  constexpr int D = MSUB + C::kOtherCopies;  // copies per wave and group
   const int G = c.G;
-#pragma unroll
-  for (int d = 0; d < kStages - 1; ++d)
-    if (d < G) issue_group<W, TILED>(c, d);
-
+  issue_group<TILED, MSUB>(c, 0);
+  issue_group<TILED, MSUB>(c, min(1, G - 1));
   for (int g = 0; g < G; ++g) {
-    wait_group<kDmaPerGroup<W, TILED>>(min(kStages - 2, G - 1 - g));
+    // group g's copies have landed once only group g+1's are outstanding;
+    // stage (g+2) % 3 was last read in iteration g-1, which every wave has
+    // left once past the barrier
+    wait_vmem<D>();
     __builtin_amdgcn_s_barrier();
-    if (g + kStages - 1 < G) issue_group<W, TILED>(c, g + kStages - 1);
-
+    const int cg = min(g + 2, G - 1);
     const char* st = smem + (g % kStages) * C::kStageBytes;
-    // this lane's codes, scales and biases for its two columns
-    const uint4 raw0 = *reinterpret_cast<const uint4*>(st + kBOff + (c.wave * 2 + 0) * 1024 + c.lane * 16);
-    const uint4 raw1 = *reinterpret_cast<const uint4*>(st + kBOff + (c.wave * 2 + 1) * 1024 + c.lane * 16);
-    const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + kSOff + c.wave * 512);
-    float s0, s1, z0, z1;
-    if constexpr (TILED) {
-      const uint32_t v0 = sw[c.l32], v1 = sw[c.l32 + 32];
-      s0 = __uint_as_float(v0 << 16);
-      z0 = __uint_as_float(v0 & 0xFFFF0000u);
-      s1 = __uint_as_float(v1 << 16);
-      z1 = __uint_as_float(v1 & 0xFFFF0000u);
-    } else {
-      const int sh = (g & 1) ? 16 : 0;
-      s0 = __uint_as_float((sw[c.l32] >> sh) << 16);
-      s1 = __uint_as_float((sw[c.l32 + 32] >> sh) << 16);
-      z0 = __uint_as_float((sw[64 + c.l32] >> sh) << 16);
-      z1 = __uint_as_float((sw[64 + c.l32 + 32] >> sh) << 16);
+    const WState ws = load_wstate<TILED>(c, st, g);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) step<TILED, MSUB, true>(c, ws, st + C::kAOff, kk, cg, acc);
+  }
+  wait_vmem<0>();  // the trailing repeat copies
+}
+
+// Order of the work: tiles ranked by subtile count, largest first (stable in
+// tile order), unit u = rank * NB + column block.  Persistent blocks take
+// units in a snake over their slots -- round k gives unit k * P + q to slot q
+// on even rounds and k * P + P - 1 - q on odd ones -- which balances the
+// largest units first and leaves the smallest for the tail.  Slot q sits on
+// XCD q / (P / 8) (block ids are dealt round-robin to the 8 XCDs), so the
+// column blocks of one tile, consecutive units, share an XCD's L2.
+constexpr int kMaxOrder = 512;  // tiles ranked in LDS; more fall back to tile order
+
+__device__ __forceinline__ int tile_msub(const GemmArgs& a, int t) {
+  const int e = min(max(a.tile_exp[t], 0), a.num_experts - 1);
+  const int64_t row0 = a.tile_row[t];
+  const int64_t rowend = min((int64_t)a.offsets[e + 1], a.n_rows);
+  const int64_t valid = min((int64_t)kBM, rowend - row0);
+  return valid <= 0 ? 0 : (int)((valid + 31) / 32);
+}
+
+__device__ void rank_tiles(const GemmArgs& a, int* order, int ntiles, int* cls_lds) {
+  // cls_lds: [kMaxOrder] subtile counts; wave 0 ranks them with ballots
+  for (int t = threadIdx.x; t < ntiles; t += kThreads) cls_lds[t] = tile_msub(a, t);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int total[kMaxSub + 1];
+#pragma unroll
+    for (int m = 0; m <= kMaxSub; ++m) total[m] = 0;
+    for (int t0 = 0; t0 < ntiles; t0 += 64) {
+      const int m = t0 + lane < ntiles ? cls_lds[t0 + lane] : -1;
+#pragma unroll
+      for (int k = 0; k <= kMaxSub; ++k) total[k] += __popcll(__ballot(m == k));
     }
-    const uint32_t w0[4] = {raw0.x, raw0.y, raw0.z, raw0.w};
-    const uint32_t w1[4] = {raw1.x, raw1.y, raw1.z, raw1.w};
-    const char* abuf = st + kAOff;
+    int start[kMaxSub + 1];
+    int acc = 0;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const i32x4_t b0 = dequant_word(w0[kk], s0, z0);
-      const i32x4_t b1 = dequant_word(w1[kk], s1, z1);
-      i32x4_t af[MSUB];
+    for (int k = kMaxSub; k >= 0; --k) {
+      start[k] = acc;
+      acc += total[k];
+    }
+    for (int t0 = 0; t0 < ntiles; t0 += 64) {
+      const int m = t0 + lane < ntiles ? cls_lds[t0 + lane] : -1;
+      int r = 0;
 #pragma unroll
-      for (int i = 0; i < MSUB; ++i) {
-        const int row = 32 * i + c.l32;  // swz(row) == swz(l32): 32*i leaves bits 0..3 alone
-        const int unit = (4 * c.h + kk) ^ swz(c.l32);
-        af[i] = *reinterpret_cast<const i32x4_t*>(abuf + row * 128 + unit * 16);
+      for (int k = 0; k <= kMaxSub; ++k) {
+        const uint64_t bal = __ballot(m == k);
+        if (m == k) r = start[k] + __popcll(bal & below);
+        start[k] += __popcll(bal);
       }
+      if (m >= 0) order[r] = t0 + lane;
+    }
+  }
+  __syncthreads();
+}
+
+template <bool TILED>
+__device__ __forceinline__ void store_tile(const GemmArgs& a, char* smem, const Ctx<TILED>& c,
+                                           const f32x16_t (&acc)[kMaxSub][2], int64_t row0, int valid, int msub,
+                                           int nblk) {
+  constexpr int kPassRows = 64;
+  char* ep = smem;  // the ring is free once every wave has left the main loop
+  const int tid = threadIdx.x;
+  uint16_t* obase = a.out + row0 * (int64_t)a.N + nblk * kBN;
+  for (int p = 0; 2 * p < msub; ++p) {
+    __syncthreads();  // the ring (first pass) or the previous pass's rows are no longer read
 #pragma unroll
-      for (int i = 0; i < MSUB; ++i) {
-        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, af[i]),
-                                                            __builtin_bit_cast(bf16x8_t, b0), acc[i][0], 0, 0, 0);
-        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, af[i]),
-                                                            __builtin_bit_cast(bf16x8_t, b1), acc[i][1], 0, 0, 0);
-      }
+    for (int i = 0; i < kMaxSub; ++i) {
+      if ((i >> 1) != p) continue;
+      const int m = 32 * (i & 1) + c.l32;  // row within the pass; m & 31 == l32
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int gi = (c.wave * 64 + 32 * j + 8 * q + 4 * c.h) / 4;  // 8-byte granule within the row
+          const uint2 v = make_uint2(cvt_pk_bf16(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                     cvt_pk_bf16(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
+          *reinterpret_cast<uint2*>(ep + m * 512 + (gi ^ (2 * c.l32)) * 8) = v;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kPassRows * 32 / kThreads; ++it) {
+      const int m = it * (kThreads / 32) + tid / 32;
+      const int u = tid % 32;
+      const int row = kPassRows * p + m;
+      const uint4 v = *reinterpret_cast<const uint4*>(ep + m * 512 + ((u ^ (m & 31)) * 16));
+      if (row < valid) *reinterpret_cast<uint4*>(obase + (int64_t)row * a.N + u * 8) = v;
     }
   }
 }
 
-template <int W, bool TILED>
-__global__ __launch_bounds__(Cfg<W>::kThreads, Cfg<W>::kBlocksPerCU) void gemm_bf16_kernel(GemmArgs a) {
-  using C = Cfg<W>;
-  constexpr int kBN = C::kBN, kWaves = C::kWaves;
-  __shared__ __attribute__((aligned(1024))) char smem[C::kStages * C::kStageBytes];
-
-  const int NB = a.N / kBN;
-  const int64_t n_active = (int64_t)a.ntiles[0] * NB;
-  const int64_t hw = blockIdx.x;
-  if (hw >= n_active) return;
-  // XCD-aware order: hardware block ids are dealt round-robin to the 8 XCDs;
-  // give each XCD a contiguous run of (tile, column block) units so the
-  // tiles of one expert share that XCD's L2.
-  const int64_t q8 = n_active / 8, r8 = n_active % 8, xcd = hw % 8;
-  const int64_t logical = xcd * q8 + (xcd < r8 ? xcd : r8) + hw / 8;
-  const int tile = (int)(logical / NB);
-  const int nblk = (int)(logical % NB);
-
+template <bool TILED>
+__device__ __forceinline__ void run_unit(const GemmArgs& a, char* smem, int tile, int nblk) {
   const int e = min(max(a.tile_exp[tile], 0), a.num_experts - 1);
   const int64_t row0 = a.tile_row[tile];
   const int64_t rowend = min((int64_t)a.offsets[e + 1], a.n_rows);
@@ -289,28 +413,24 @@ __global__ __launch_bounds__(Cfg<W>::kThreads, Cfg<W>::kBlocksPerCU) void gemm_b
   const int64_t KW = K / 8;
   const int tid = threadIdx.x;
 
-  Ctx<W> c;
+  Ctx<TILED> c;
   c.G = G;
   c.wave = __builtin_amdgcn_readfirstlane(tid / 64);
   c.lane = tid % 64;
   c.l32 = c.lane % 32;
   c.h = c.lane / 32;
   c.lds = (uint32_t)(uintptr_t)smem;
-  // A copies: wave w, copy q writes stage units (q*kWaves + w)*64 + lane, i.e.
-  // row p/8 and stored unit p%8, which holds logical unit (p%8) ^ swz(row).
+  // A copy q of wave w writes stage bytes (4q + w) * 1024 + lane * 16: row
+  // 32q + 8w + lane/8, stored unit lane%8, which holds logical unit
+  // (lane%8) ^ swz(row).  Rows past the tile repeat its last valid row.
 #pragma unroll
-  for (int q = 0; q < C::kACopies; ++q) {
-    const int p = (q * kWaves + c.wave) * 64 + c.lane;
-    const int row = p >> 3;
-    const int unit = (p & 7) ^ swz(row);
+  for (int q = 0; q < kMaxSub; ++q) {
+    const int row = 32 * q + 8 * c.wave + (c.lane >> 3);
+    const int unit = (c.lane & 7) ^ swz(row);
     int64_t src = row0 + min(row, valid - 1);
     if (a.x_rows) src = a.x_rows[src];
     c.a_src[q] = reinterpret_cast<const char*>(a.x + src * K + unit * 8);
-    c.a_dst[q] = (uint32_t)(C::kAOff + (q * kWaves + c.wave) * 1024);
   }
-  const int64_t col_base = (int64_t)e * a.N + nblk * kBN + c.wave * 64;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) c.b_dst[j] = (uint32_t)(C::kBOff + (c.wave * 2 + j) * 1024);
   if constexpr (TILED) {
     // chunk (e, c, g) of the tile layout, c = the wave's 64-column block
     const int64_t chunk0 = ((int64_t)e * (a.N / 64) + nblk * kWaves + c.wave) * G;
@@ -320,46 +440,80 @@ __global__ __launch_bounds__(Cfg<W>::kThreads, Cfg<W>::kBlocksPerCU) void gemm_b
     c.s_src = reinterpret_cast<const char*>(a.sb) + chunk0 * 256 + c.lane * 4;
     c.z_src = nullptr;
   } else {
+    const int64_t col_base = (int64_t)e * a.N + nblk * kBN + c.wave * 64;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       c.b_src[j] = reinterpret_cast<const char*>(a.w + (col_base + j * 32 + c.l32) * KW + c.h * 4);
     c.s_src = reinterpret_cast<const char*>(a.s + (col_base + c.lane) * G);
     c.z_src = reinterpret_cast<const char*>(a.b + (col_base + c.lane) * G);
   }
-  c.s_dst = (uint32_t)(C::kSOff + c.wave * 512);
-  c.z_dst = c.s_dst + 256;
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[kMaxSub][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kMaxSub; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   switch (msub) {
-    case 1: tile_loop<W, TILED, 1>(c, smem, acc); break;
-    case 2: tile_loop<W, TILED, 2>(c, smem, acc); break;
-    case 3: tile_loop<W, TILED, 3>(c, smem, acc); break;
-    default: tile_loop<W, TILED, 4>(c, smem, acc); break;
+    case 1: tile_loop<TILED, 1>(c, smem, acc); break;
+    case 2: tile_loop<TILED, 2>(c, smem, acc); break;
+    case 3: tile_loop<TILED, 3>(c, smem, acc); break;
+    case 4: tile_loop<TILED, 4>(c, smem, acc); break;
+    case 5: tile_loop<TILED, 5>(c, smem, acc); break;
+    case 6: tile_loop<TILED, 6>(c, smem, acc); break;
+    case 7: tile_loop<TILED, 7>(c, smem, acc); break;
+    default: tile_loop<TILED, 8>(c, smem, acc); break;
   }
 
-  // epilogue: D[m][n] of a 32x32 subtile sits in lane n (mod 32), register
-  // r at row 8*(r/4) + 4*(lane/32) + r%4.
-  const int ncol = nblk * kBN + c.wave * 64 + c.l32;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (i >= msub) continue;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = 32 * i + 8 * (r / 4) + 4 * c.h + (r % 4);
-      if (m < valid) {
-        uint16_t* orow = a.out + (row0 + m) * (int64_t)a.N + ncol;
-        orow[0] = (uint16_t)f32_to_bf16(acc[i][0][r]);
-        orow[32] = (uint16_t)f32_to_bf16(acc[i][1][r]);
-      }
-    }
+  // epilogue: subtile (i, j) holds D^T -- lane l32 is token row 32i + l32,
+  // register r is output column 32j + 8(r/4) + 4h + r%4.  The tile goes out
+  // through LDS, 64 rows at a time, so that each store instruction writes
+  // whole 512-byte row segments (the block's 256 columns) instead of 32
+  // scattered 16-byte pieces: every wave writes its 8-byte column quads into
+  // a row-major staging area (16-byte unit u of row m at u ^ (m & 31), which
+  // keeps both the quad writes and the 16-byte row reads spread over the
+  // banks), then the block stores the rows.
+  store_tile<TILED>(a, smem, c, acc, row0, valid, msub, nblk);
+}
+
+// Persistent grid: P blocks (a multiple of 8, one per CU), each walking its
+// slot's units of the ranked order.
+template <bool TILED>
+__global__ __launch_bounds__(kThreads, kBlocksPerCU) void gemm_bf16_kernel(GemmArgs a) {
+  using C = Cfg<TILED>;
+  __shared__ __attribute__((aligned(1024))) char smem[C::kLdsBytes];
+  __shared__ int order[kMaxOrder];
+
+  const int NB = a.N / kBN;
+  const int ntiles = a.ntiles[0];
+  const int64_t units = (int64_t)ntiles * NB;
+  const int P = gridDim.x;
+  const int blk = blockIdx.x;
+  const int q = (blk % 8) * (P / 8) + blk / 8;
+  if (q >= units) return;
+  const bool sorted = ntiles <= kMaxOrder;
+  if (sorted) rank_tiles(a, order, ntiles, reinterpret_cast<int*>(smem));  // the ring is free until the first unit
+  for (int64_t k = 0;; ++k) {
+    const int64_t u = k * P + ((k & 1) ? P - 1 - q : q);
+    if (u >= units) break;
+    const int rank = (int)(u / NB);
+    const int tile = sorted ? order[rank] : rank;
+    __syncthreads();  // every wave is done with the ring before it is refilled
+    run_unit<TILED>(a, smem, tile, (int)(u % NB));
   }
+}
+
+int num_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cus = n;
+    if (cus <= 0) cus = 256;
+  }
+  return cus;
 }
 
 }  // namespace
@@ -369,15 +523,13 @@ extern "C" int qmoe_gemm_tile_rows(void) { return kBM; }
 namespace {
 
 int launch_gemm(const GemmArgs& a, int64_t max_tiles, bool tiled, void* stream) {
-  const bool wide = a.N % Cfg<8>::kBN == 0;
-  const int64_t blocks = max_tiles * (a.N / (wide ? Cfg<8>::kBN : Cfg<4>::kBN));
-  if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
-  const dim3 grid((unsigned)blocks);
+  // one block per CU, a multiple of 8 (the XCD count), never more than the units
+  const int64_t units = max_tiles * (a.N / kBN);
+  const int64_t P = std::max<int64_t>(8, std::min<int64_t>((kBlocksPerCU * num_cus() + 7) / 8 * 8, (units + 7) / 8 * 8));
+  const dim3 grid((unsigned)P);
   hipStream_t st = qmoe::as_stream(stream);
-  if (wide && tiled) gemm_bf16_kernel<8, true><<<grid, dim3(Cfg<8>::kThreads), 0, st>>>(a);
-  else if (wide) gemm_bf16_kernel<8, false><<<grid, dim3(Cfg<8>::kThreads), 0, st>>>(a);
-  else if (tiled) gemm_bf16_kernel<4, true><<<grid, dim3(Cfg<4>::kThreads), 0, st>>>(a);
-  else gemm_bf16_kernel<4, false><<<grid, dim3(Cfg<4>::kThreads), 0, st>>>(a);
+  if (tiled) gemm_bf16_kernel<true><<<grid, dim3(kThreads), 0, st>>>(a);
+  else gemm_bf16_kernel<false><<<grid, dim3(kThreads), 0, st>>>(a);
   return qmoe::launch_status("gemm_bf16_kernel");
 }
 
@@ -388,8 +540,9 @@ int check_common(const uint16_t* x, int64_t n_rows, int64_t K, int32_t num_exper
     return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
   if (n_rows == 0 || max_tiles == 0) return QMOE_OK;
   if (!x || !offsets || !tile_row || !tile_exp || !ntiles || !out) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
-  if (N % 256) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of 256", (long long)N);
+  if (N % kBN) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of %d", (long long)N, kBN);
   if (!qmoe::aligned16(x)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x must be 16-byte aligned");
+  if (!qmoe::aligned16(out)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "out must be 16-byte aligned");
   if (K > 0x7FFFFFFF || N > 0x7FFFFFFF || n_rows > 0x7FFFFFFF)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
   return QMOE_OK;

@@ -18,6 +18,7 @@
 
 namespace {
 
+constexpr int kTileRows = 128;  // rows per routing tile (qmoe_gemm_tile_rows)
 constexpr int kBM = 128;
 constexpr int kBN = 256;
 constexpr int kThreads = 256;
@@ -108,17 +109,20 @@ __global__ __launch_bounds__(kThreads) void gemm_int8_kernel(Int8Args a) {
   __shared__ __attribute__((aligned(16))) uint16_t Rhi[kBM][kMaxG + 8];
   __shared__ __attribute__((aligned(16))) uint16_t Rlo[kBM][kMaxG + 8];
 
+  // A routing tile spans up to kTileRows rows; a block covers kBM of them.
   const int NB = a.N / kBN;
-  const int64_t n_active = (int64_t)a.ntiles[0] * NB;
+  constexpr int kHalves = kTileRows / kBM;
+  const int64_t n_active = (int64_t)a.ntiles[0] * kHalves * NB;
   const int64_t hw = blockIdx.x;
   if (hw >= n_active) return;
   const int64_t q8 = n_active / 8, r8 = n_active % 8, xcd = hw % 8;
   const int64_t logical = xcd * q8 + (xcd < r8 ? xcd : r8) + hw / 8;
-  const int tile = (int)(logical / NB);
+  const int tile = (int)(logical / (NB * kHalves));
+  const int half = (int)(logical / NB % kHalves);
   const int nblk = (int)(logical % NB);
 
   const int e = min(max(a.tile_exp[tile], 0), a.num_experts - 1);
-  const int64_t row0 = a.tile_row[tile];
+  const int64_t row0 = a.tile_row[tile] + (int64_t)half * kBM;
   const int64_t rowend = min((int64_t)a.offsets[e + 1], a.n_rows);
   const int valid = (int)min((int64_t)kBM, rowend - row0);
   if (valid <= 0) return;
@@ -311,7 +315,8 @@ extern "C" int qmoe_gather_qmm_int8_sorted(const int8_t* xi, const float* sx, co
   if (!qmoe::aligned16(xi) || !qmoe::aligned16(w) || !qmoe::aligned16(scales) || !qmoe::aligned16(biases))
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "xi, w, scales and biases must be 16-byte aligned");
   if (N > 0x7FFFFFFF || n_rows > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
-  const int64_t blocks = max_tiles * (N / kBN);
+  if (qmoe_gemm_tile_rows() != kTileRows) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "tile rows mismatch");
+  const int64_t blocks = max_tiles * (kTileRows / kBM) * (N / kBN);
   if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
   Int8Args a{xi, sx, x_rows, n_rows, (int)K, w, scales, biases, num_experts, (int)N, offsets, tile_row, tile_exp,
              ntiles, out};
