@@ -244,6 +244,20 @@ int qmoe_gather_qmm_int8_sorted(const int8_t* xi, const float* sx,
                                 int64_t max_tiles, uint16_t* out,
                                 void* stream);
 
+/* qmoe_gather_qmm_int8_sorted over tile-layout weights (wp, sb from
+ * qmoe_repack_tiles); same rows, tiles and arithmetic.  Replaces the same
+ * reference op (titan/kernels/moe_gather_int8.py:393-425) with the prepared
+ * tables (:189-248) in the role of the tile layout. */
+int qmoe_gather_qmm_int8_sorted_tiles(const int8_t* xi, const float* sx,
+                                      const int32_t* x_rows, int64_t n_rows,
+                                      int64_t K, const uint32_t* wp,
+                                      const uint32_t* sb, int32_t num_experts,
+                                      int64_t N, const int32_t* offsets,
+                                      const int32_t* tile_row,
+                                      const int32_t* tile_exp,
+                                      const int32_t* ntiles, int64_t max_tiles,
+                                      uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -354,16 +354,42 @@ def test_quantize_act_int8_bit_exact(dev, orc):
     assert np.array_equal(xi.cpu().numpy(), rxi)
 
 
-@pytest.mark.parametrize("E,N,K,R", [(8, 256, 1024, 300), (16, 512, 2048, 640)])
+@pytest.mark.parametrize("E,N,K,R", [(8, 256, 1024, 300), (16, 512, 2048, 640), (4, 768, 4096, 200),
+                                     (8, 256, 1536, 90)])
 def test_sorted_gemm_int8(dev, orc, E, N, K, R):
     say(f"int8 sorted GEMM E={E} N={N} K={K} R={R}")
     w, s, b, ids, x = _sorted_problem(E * 17 + R, E, N, K, R)
     xi, sx = ops.quantize_act_int8(bf16_t(x, dev))
     tiles = ops.build_tiles(i32_t(ids, dev), E)
-    y = ops.gather_qmm_int8_sorted(xi, sx, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
     rxi, rsx = orc.quant_act_int8(x)
     ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, None, ids, w, s, b)
-    assert_close_bf16(orc, bits(y), ref64, what=f"int8 gemm {E}/{N}/{K}/{R}")
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    yt = ops.gather_qmm_int8_sorted_tiles(xi, sx, tw, tiles)
+    assert_close_bf16(orc, bits(yt), ref64, what=f"int8 gemm tiles {E}/{N}/{K}/{R}")
+    if K % 128 == 0:
+        y = ops.gather_qmm_int8_sorted(xi, sx, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
+        assert_close_bf16(orc, bits(y), ref64, what=f"int8 gemm {E}/{N}/{K}/{R}")
+        # same rows, groups and summation order: the layouts agree bit for bit
+        assert np.array_equal(bits(y), bits(yt))
+
+
+def test_sorted_gemm_int8_every_subtile_count(dev, orc):
+    """Experts with 1, 17, 33, ... rows: tiles of every 16- and 32-row subtile
+    count, a full tile and a tile boundary inside an expert."""
+    counts = [1, 17, 33, 49, 65, 81, 97, 113, 128, 200, 0, 31]
+    E, N, K = len(counts), 512, 512
+    say("int8 sorted GEMM every subtile count")
+    rng = np.random.default_rng(6)
+    w, s, b = synth.quant_weights(rng, (E, N), K)
+    ids = np.repeat(np.arange(E), counts).astype(np.int32)
+    x = synth.bf16_bits(rng.normal(size=(len(ids), K)).astype(np.float32))
+    xi, sx = ops.quantize_act_int8(bf16_t(x, dev))
+    tiles = ops.build_tiles(i32_t(ids, dev), E)
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    y = ops.gather_qmm_int8_sorted_tiles(xi, sx, tw, tiles)
+    rxi, rsx = orc.quant_act_int8(x)
+    ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, None, ids, w, s, b)
+    assert_close_bf16(orc, bits(y), ref64, what="int8 gemm every subtile count")
 
 
 def test_sorted_gemm_int8_cfg4_sampled(dev, orc):
@@ -374,8 +400,8 @@ def test_sorted_gemm_int8_cfg4_sampled(dev, orc):
     xi, sx = ops.quantize_act_int8(bf16_t(wl["x"], dev))
     r = ops.route(i32_t(ids, dev), 256)
     lhs = torch.div(r.order, k, rounding_mode="floor").to(torch.int32)
-    y = ops.gather_qmm_int8_sorted(xi, sx, words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev),
-                                   r.tiles, x_rows=lhs)
+    tw = ops.repack_tiles(words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev))
+    y = ops.gather_qmm_int8_sorted_tiles(xi, sx, tw, r.tiles, x_rows=lhs)
     torch.cuda.synchronize()
     order, _, srt = orc.route_sort(ids, 256)
     off = np.searchsorted(srt, np.arange(257), side="left")

@@ -68,6 +68,7 @@ SIGNATURES: dict[str, tuple] = {
     "qmoe_quantize_act_int8": (INT, [P, I64, I64, P, P, P]),
     "qmoe_gather_qmm_int8_sorted": (INT, [P, P, P, I64, I64, P, P, P, I32, I64, INT, INT, P, P, P, P,
                                           I64, P, P]),
+    "qmoe_gather_qmm_int8_sorted_tiles": (INT, [P, P, P, I64, I64, P, P, I32, I64, P, P, P, P, I64, P, P]),
 }
 
 _lock = threading.Lock()

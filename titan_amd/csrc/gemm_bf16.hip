@@ -41,20 +41,19 @@
 // K order inside a group is free as long as A and B agree: lane half h
 // supplies group elements 32h + 8kk .. +7 at k-step kk -- word kk of the
 // lane's 16-byte code chunk and 16-byte unit 4h + kk of the activation row.
-#include <algorithm>
 #include <type_traits>
 
-#include "common.h"
+#include "gemm_common.h"
 
 namespace {
 
-constexpr int kBM = 128;
-constexpr int kMaxSub = kBM / 32;
+using namespace qmoe_gemm;
+
+constexpr int kBM = kTileRows;
 constexpr int kWaves = 4;
 constexpr int kBN = 64 * kWaves;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kStages = 3;
-constexpr int kBlocksPerCU = 2;
+static_assert(kThreads == 64 * kWaves, "four waves per block");
 
 // Stage layout (bytes).  TILED: one scale|bias word per column; MLX layout:
 // a scale pair and a bias pair (two groups) per column.
@@ -68,7 +67,7 @@ struct Cfg {
   static constexpr int kSBytes = kWaves * (TILED ? 1 : 2) * 64 * 4;
   static constexpr int kStageBytes = kSOff + kSBytes;
   static constexpr int kLdsBytes = kStages * kStageBytes;
-  static_assert(kBlocksPerCU * (kLdsBytes + 4 * 512) <= 160 * 1024, "LDS per CU");
+  static_assert(kBlocksPerCU * (kLdsBytes + 4 * kMaxOrder) <= 160 * 1024, "LDS per CU");
   // copies per wave and group besides A: two code chunks, one (tiled) or two
   // (scale pair, bias pair) scale copies
   static constexpr int kOtherCopies = 2 + (TILED ? 1 : 2);
@@ -91,38 +90,6 @@ struct GemmArgs {
   const int32_t* ntiles;
   uint16_t* out;
 };
-
-// Asynchronous 16- and 4-byte copies into LDS: lane i writes
-// lds_base + i * size.  M0 carries the LDS base (declared clobbered).
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off"
-      :
-      : "s"(lds_base), "v"(g)
-      : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dword %1, off"
-      :
-      : "s"(lds_base), "v"(g)
-      : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
-
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
-  f32x2_t v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-}
 
 // fma(h, s, b) in fp32 with h the fp16 in the low (HI = false) or high half
 // of v, widened exactly (fp16 denormals included): one v_fma_mix_f32.
@@ -309,60 +276,6 @@ __device__ __forceinline__ void tile_loop(const Ctx<TILED>& c, const char* smem,
   wait_vmem<0>();  // the trailing repeat copies
 }
 
-// Order of the work: tiles ranked by subtile count, largest first (stable in
-// tile order), unit u = rank * NB + column block.  Persistent blocks take
-// units in a snake over their slots -- round k gives unit k * P + q to slot q
-// on even rounds and k * P + P - 1 - q on odd ones -- which balances the
-// largest units first and leaves the smallest for the tail.  Slot q sits on
-// XCD q / (P / 8) (block ids are dealt round-robin to the 8 XCDs), so the
-// column blocks of one tile, consecutive units, share an XCD's L2.
-constexpr int kMaxOrder = 512;  // tiles ranked in LDS; more fall back to tile order
-
-__device__ __forceinline__ int tile_msub(const GemmArgs& a, int t) {
-  const int e = min(max(a.tile_exp[t], 0), a.num_experts - 1);
-  const int64_t row0 = a.tile_row[t];
-  const int64_t rowend = min((int64_t)a.offsets[e + 1], a.n_rows);
-  const int64_t valid = min((int64_t)kBM, rowend - row0);
-  return valid <= 0 ? 0 : (int)((valid + 31) / 32);
-}
-
-__device__ void rank_tiles(const GemmArgs& a, int* order, int ntiles, int* cls_lds) {
-  // cls_lds: [kMaxOrder] subtile counts; wave 0 ranks them with ballots
-  for (int t = threadIdx.x; t < ntiles; t += kThreads) cls_lds[t] = tile_msub(a, t);
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int total[kMaxSub + 1];
-#pragma unroll
-    for (int m = 0; m <= kMaxSub; ++m) total[m] = 0;
-    for (int t0 = 0; t0 < ntiles; t0 += 64) {
-      const int m = t0 + lane < ntiles ? cls_lds[t0 + lane] : -1;
-#pragma unroll
-      for (int k = 0; k <= kMaxSub; ++k) total[k] += __popcll(__ballot(m == k));
-    }
-    int start[kMaxSub + 1];
-    int acc = 0;
-#pragma unroll
-    for (int k = kMaxSub; k >= 0; --k) {
-      start[k] = acc;
-      acc += total[k];
-    }
-    for (int t0 = 0; t0 < ntiles; t0 += 64) {
-      const int m = t0 + lane < ntiles ? cls_lds[t0 + lane] : -1;
-      int r = 0;
-#pragma unroll
-      for (int k = 0; k <= kMaxSub; ++k) {
-        const uint64_t bal = __ballot(m == k);
-        if (m == k) r = start[k] + __popcll(bal & below);
-        start[k] += __popcll(bal);
-      }
-      if (m >= 0) order[r] = t0 + lane;
-    }
-  }
-  __syncthreads();
-}
-
 template <bool TILED>
 __device__ __forceinline__ void store_tile(const GemmArgs& a, char* smem, const Ctx<TILED>& c,
                                            const f32x16_t (&acc)[kMaxSub][2], int64_t row0, int valid, int msub,
@@ -401,10 +314,9 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, char* smem, const 
 
 template <bool TILED>
 __device__ __forceinline__ void run_unit(const GemmArgs& a, char* smem, int tile, int nblk) {
-  const int e = min(max(a.tile_exp[tile], 0), a.num_experts - 1);
-  const int64_t row0 = a.tile_row[tile];
-  const int64_t rowend = min((int64_t)a.offsets[e + 1], a.n_rows);
-  const int valid = (int)min((int64_t)kBM, rowend - row0);
+  const TileRows tr = tile_rows_of(Tiles{a.offsets, a.tile_row, a.tile_exp, a.ntiles, a.n_rows, a.num_experts}, tile);
+  const int e = tr.e, valid = tr.valid;
+  const int64_t row0 = tr.row0;
   if (valid <= 0) return;
   const int msub = (valid + 31) / 32;
 
@@ -478,42 +390,28 @@ __device__ __forceinline__ void run_unit(const GemmArgs& a, char* smem, int tile
   store_tile<TILED>(a, smem, c, acc, row0, valid, msub, nblk);
 }
 
-// Persistent grid: P blocks (a multiple of 8, one per CU), each walking its
-// slot's units of the ranked order.
+// Persistent grid (kBlocksPerCU blocks per CU), each block walking its
+// slot's units of the ranked tile order.
 template <bool TILED>
 __global__ __launch_bounds__(kThreads, kBlocksPerCU) void gemm_bf16_kernel(GemmArgs a) {
   using C = Cfg<TILED>;
   __shared__ __attribute__((aligned(1024))) char smem[C::kLdsBytes];
   __shared__ int order[kMaxOrder];
 
+  const Tiles tt{a.offsets, a.tile_row, a.tile_exp, a.ntiles, a.n_rows, a.num_experts};
   const int NB = a.N / kBN;
   const int ntiles = a.ntiles[0];
-  const int64_t units = (int64_t)ntiles * NB;
-  const int P = gridDim.x;
-  const int blk = blockIdx.x;
-  const int q = (blk % 8) * (P / 8) + blk / 8;
-  if (q >= units) return;
+  const Snake sn((int64_t)ntiles * NB);
+  if (sn.unit(0) < 0) return;
   const bool sorted = ntiles <= kMaxOrder;
-  if (sorted) rank_tiles(a, order, ntiles, reinterpret_cast<int*>(smem));  // the ring is free until the first unit
+  if (sorted) rank_tiles(tt, ntiles, order, reinterpret_cast<int*>(smem));  // the ring is free until the first unit
   for (int64_t k = 0;; ++k) {
-    const int64_t u = k * P + ((k & 1) ? P - 1 - q : q);
-    if (u >= units) break;
+    const int64_t u = sn.unit(k);
+    if (u < 0) break;
     const int rank = (int)(u / NB);
-    const int tile = sorted ? order[rank] : rank;
     __syncthreads();  // every wave is done with the ring before it is refilled
-    run_unit<TILED>(a, smem, tile, (int)(u % NB));
+    run_unit<TILED>(a, smem, sorted ? order[rank] : rank, (int)(u % NB));
   }
-}
-
-int num_cus() {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-      cus = n;
-    if (cus <= 0) cus = 256;
-  }
-  return cus;
 }
 
 }  // namespace
@@ -523,10 +421,7 @@ extern "C" int qmoe_gemm_tile_rows(void) { return kBM; }
 namespace {
 
 int launch_gemm(const GemmArgs& a, int64_t max_tiles, bool tiled, void* stream) {
-  // one block per CU, a multiple of 8 (the XCD count), never more than the units
-  const int64_t units = max_tiles * (a.N / kBN);
-  const int64_t P = std::max<int64_t>(8, std::min<int64_t>((kBlocksPerCU * num_cus() + 7) / 8 * 8, (units + 7) / 8 * 8));
-  const dim3 grid((unsigned)P);
+  const dim3 grid((unsigned)grid_blocks(max_tiles * (a.N / kBN)));
   hipStream_t st = qmoe::as_stream(stream);
   if (tiled) gemm_bf16_kernel<true><<<grid, dim3(kThreads), 0, st>>>(a);
   else gemm_bf16_kernel<false><<<grid, dim3(kThreads), 0, st>>>(a);
@@ -586,3 +481,20 @@ extern "C" int qmoe_gather_qmm_sorted_tiles(const uint16_t* x, const int32_t* x_
              tile_exp, ntiles, out};
   return launch_gemm(a, max_tiles, true, stream);
 }
+
+namespace qmoe_gemm {
+
+int grid_blocks(int64_t units, int blocks_per_cu) {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cus = n;
+    if (cus <= 0) cus = 256;
+  }
+  const int64_t full = ((int64_t)blocks_per_cu * cus + 7) / 8 * 8;
+  const int64_t need = (units + 7) / 8 * 8;
+  return (int)(need < full ? (need < 8 ? 8 : need) : full);
+}
+
+}  // namespace qmoe_gemm

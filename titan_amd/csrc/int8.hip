@@ -12,18 +12,10 @@
 //   y[m, n]   = sx[m] * ( sum_g s[n,g] * D_g[m,n]  +  sum_g b[n,g] * R_g[m] )
 // The first sum is rescaled in fp32 after every group; the second is a
 // [rows x G] x [G x N] product run once at the end on bf16 MFMA with R split
-// into two bf16 terms (|R| <= 8128: hi = bf16(R) and lo = R - hi are exact),
-// so it adds no per-group vector work.
-#include "common.h"
+// into two bf16 terms (|R| <= 8128: hi = bf16(R) and lo = R - hi are exact).
+#include "gemm_common.h"
 
 namespace {
-
-constexpr int kTileRows = 128;  // rows per routing tile (qmoe_gemm_tile_rows)
-constexpr int kBM = 128;
-constexpr int kBN = 256;
-constexpr int kThreads = 256;
-constexpr int kLDA = 80;   // bytes per LDS activation row: 64 + 16 pad
-constexpr int kMaxG = 64;  // K <= 4096
 
 // ---------------------------------------------------------------- quantizer
 
@@ -63,6 +55,66 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restri
 }
 
 // ---------------------------------------------------------------- GEMM
+//
+// Work unit: one (128-row tile, 256-column block); a block's eight waves
+// (two per SIMD) own 32 columns each and all the tile's rows.  Persistent
+// blocks, one per CU, take units heavy-first (gemm_common.h).  Per 64-wide K group g every
+// operand byte reaches LDS through asynchronous copies into a ring of three
+// stages:
+//   A  the tile's int8 activation rows, 128 x 64 bytes, gathered through
+//      x_rows, 16-byte unit u of row r stored at u ^ aswz(r);
+//   B  each wave's 32 columns of packed codes (tile layout: half a 2 KiB
+//      chunk; MLX layout: 16 bytes per lane from the column's row);
+//   S  the columns' scales and biases.
+// A wave turns its code words into int8 with byte permutes (codes 0..15 are
+// valid int8: no zero point), runs v_mfma_i32_32x32x32_i8 twice per 32 x 32
+// subtile (D_g exact in int32) and folds acc += s * D_g in fp32; the wave
+// whose index matches a row subtile also takes that subtile's exact row sums
+// R_g with v_dot4 and keeps them in LDS as int16 (|R_g| <= 64 * 127).  After
+// the last group the bias term sum_g b[n,g] R_g[m] is one small bf16 MFMA
+// product per subtile (R split into exact bf16 hi + lo), the rows are scaled
+// by sx and the tile leaves through LDS as 512-byte row segments.
+//
+// K order inside a group is free as long as both operands agree: MFMA k-half
+// kk of a group takes, for lane half h, group elements 32h + 16kk .. +15 --
+// code words 2kk, 2kk+1 of the lane's 16-byte code chunk and 16-byte unit
+// 2h + kk of the activation row.
+
+using namespace qmoe_gemm;
+
+constexpr int kBM = kTileRows;  // 128
+constexpr int kWaves = 8;        // two per SIMD: one wave's rescale fills the other's waits
+constexpr int kCols = 32;        // columns per wave
+constexpr int kBN = kCols * kWaves;
+constexpr int kI8Threads = 64 * kWaves;
+constexpr int kStages = 3;
+constexpr int kMaxG = 64;  // K <= 4096
+constexpr int kI8BlocksPerCU = 1;
+// Row sums R_g[row] live in LDS as int16 [group][kRStride]: consecutive rows
+// are consecutive halves (conflict-free for the lanes of one group), and the
+// pad shifts successive groups by one bank.
+constexpr int kRStride = kTileRows + 2;
+
+// Stage layout: A rows; B one 1 KiB code copy per wave (its 32 columns);
+// S the scale|bias words (tile layout) or scale and bias pairs (MLX layout)
+// of the 64-column block holding the wave's columns, one 256-byte copy each.
+template <bool TILED>
+struct ICfg {
+  static constexpr int kAOff = 0;
+  static constexpr int kABytes = kBM * 64;
+  static constexpr int kBOff = kAOff + kABytes;
+  static constexpr int kBBytes = kWaves * 1024;
+  static constexpr int kSOff = kBOff + kBBytes;
+  static constexpr int kSBytes = kWaves * (TILED ? 1 : 2) * 64 * 4;
+  static constexpr int kStageBytes = kSOff + kSBytes;
+  static constexpr int kRingBytes = kStages * kStageBytes;
+  static constexpr int kRBytes = kRStride * kMaxG * 2;  // int16 row sums [group][row]
+  static constexpr int kLdsBytes = kRingBytes + kRBytes + kBM * 4;  // + sx of the tile's rows
+  static_assert(kI8BlocksPerCU * (kLdsBytes + 4 * kMaxOrder) <= 160 * 1024, "LDS per CU");
+  static_assert(kRingBytes >= 64 * 512, "the epilogue stages 64 rows of 512 bytes in the ring");
+  static constexpr int kACopies = kABytes / (kWaves * 1024);  // 1 KiB copies per wave
+  static constexpr int kCopies = kACopies + 1 + (TILED ? 1 : 2);
+};
 
 struct Int8Args {
   const int8_t* xi;
@@ -70,9 +122,10 @@ struct Int8Args {
   const int32_t* x_rows;
   int64_t n_rows;
   int K;
-  const uint32_t* w;
-  const uint16_t* s;
-  const uint16_t* b;
+  const uint32_t* w;   // MLX codes, or tile-layout codes
+  const uint16_t* s;   // MLX scales (null for the tile layout)
+  const uint16_t* b;   // MLX biases
+  const uint32_t* sb;  // tile layout: scale|bias words
   int num_experts;
   int N;
   const int32_t* offsets;
@@ -80,6 +133,17 @@ struct Int8Args {
   const int32_t* tile_exp;
   const int32_t* ntiles;
   uint16_t* out;
+};
+
+template <bool TILED>
+struct ICtx {
+  const char* a_src[ICfg<TILED>::kACopies];  // activation 16-byte unit of the lane's row, group 0
+  const char* b_src;
+  const char* s_src;
+  const char* z_src;
+  uint32_t lds;
+  int G;
+  int wave, lane, l32, h;
 };
 
 // 16 codes (two words, k order 0..15) -> 16 int8 in natural k order.
@@ -94,188 +158,375 @@ __device__ __forceinline__ i32x4_t codes_to_i8(uint32_t wa, uint32_t wb) {
   return r;
 }
 
-__device__ __forceinline__ float bf16_at(const uint4& c, int i) {
-  const uint32_t w = (i & 4) ? ((i & 2) ? c.w : c.z) : ((i & 2) ? c.y : c.x);
-  return (i & 1) ? bf16hi(w) : bf16lo(w);
+template <bool TILED>
+__device__ __forceinline__ void issue_copy(const ICtx<TILED>& c, int g, int d) {
+  using C = ICfg<TILED>;
+  const uint32_t st = c.lds + (uint32_t)(g % kStages) * C::kStageBytes;
+  if (d < C::kACopies) {
+    dma16(c.a_src[d] + (size_t)g * 64, st + C::kAOff + (uint32_t)(d * kWaves + c.wave) * 1024);
+    return;
+  }
+  const int j = d - C::kACopies;
+  if constexpr (TILED) {
+    if (j == 0) dma16(c.b_src + (size_t)g * 2048, st + C::kBOff + (uint32_t)c.wave * 1024);
+    else dma4(c.s_src + (size_t)g * 256, st + C::kSOff + c.wave * 256);
+  } else {
+    if (j == 0) dma16(c.b_src + (size_t)g * 32, st + C::kBOff + (uint32_t)c.wave * 1024);
+    else if (j == 1) dma4(c.s_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.wave * 512);
+    else dma4(c.z_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.wave * 512 + 256);
+  }
 }
 
-__device__ __forceinline__ int sum_i8x4(uint32_t v) {
-  return (int)(int8_t)(v & 0xFF) + (int)(int8_t)((v >> 8) & 0xFF) + (int)(int8_t)((v >> 16) & 0xFF) +
-         (int)(int8_t)(v >> 24);
+template <bool TILED>
+__device__ __forceinline__ void issue_group(const ICtx<TILED>& c, int g) {
+#pragma unroll
+  for (int d = 0; d < ICfg<TILED>::kCopies; ++d) issue_copy<TILED>(c, g, d);
 }
 
-__global__ __launch_bounds__(kThreads) void gemm_int8_kernel(Int8Args a) {
-  __shared__ __attribute__((aligned(16))) int8_t As[2][kBM * kLDA];
-  __shared__ __attribute__((aligned(16))) uint16_t Rhi[kBM][kMaxG + 8];
-  __shared__ __attribute__((aligned(16))) uint16_t Rlo[kBM][kMaxG + 8];
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
-  // A routing tile spans up to kTileRows rows; a block covers kBM of them.
-  const int NB = a.N / kBN;
-  constexpr int kHalves = kTileRows / kBM;
-  const int64_t n_active = (int64_t)a.ntiles[0] * kHalves * NB;
-  const int64_t hw = blockIdx.x;
-  if (hw >= n_active) return;
-  const int64_t q8 = n_active / 8, r8 = n_active % 8, xcd = hw % 8;
-  const int64_t logical = xcd * q8 + (xcd < r8 ? xcd : r8) + hw / 8;
-  const int tile = (int)(logical / (NB * kHalves));
-  const int half = (int)(logical / NB % kHalves);
-  const int nblk = (int)(logical % NB);
+// Accumulators of a wave: its 32 columns as two 16-column subtiles jj and
+// the tile's rows as up to eight 16-row subtiles i; D[m][n] of a 16 x 16
+// MFMA tile sits in lane n (mod 16), register r at row 4 * (lane / 16) + r.
+constexpr int kJJ = kCols / 16;
+typedef f32x4_t Acc[2 * kMaxSub][kJJ];
 
-  const int e = min(max(a.tile_exp[tile], 0), a.num_experts - 1);
-  const int64_t row0 = a.tile_row[tile] + (int64_t)half * kBM;
-  const int64_t rowend = min((int64_t)a.offsets[e + 1], a.n_rows);
-  const int valid = (int)min((int64_t)kBM, rowend - row0);
-  if (valid <= 0) return;
-  const int msub = (valid + 31) / 32;
+// Row swizzle of the 16-byte units of a 64-byte activation row in LDS: unit
+// u of row r is stored at u ^ aswz(r).  Conflict-free for 16-byte reads of
+// one unit by consecutive rows whether the LDS serves 8 lanes per pass over
+// 32 banks (aswz takes distinct values on each parity among r .. r+7) or 16
+// lanes over 64 banks (distinct on each residue mod 4 among r .. r+15).
+__device__ __forceinline__ int aswz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
 
-  const int K = a.K;
-  const int G = K / 64;
-  const int64_t KW = K / 8;
-  const int tid = threadIdx.x;
-  const int wave = tid / 64;
-  const int lane = tid % 64;
-  const int l32 = lane % 32;
-  const int h = lane / 32;
+// Main loop over the groups of one tile with MSUB 32-row subtiles.  Per group
+// and 16 x 16 subtile one v_mfma_i32_16x16x64_i8 covers the whole group;
+// lane quarter qq supplies group elements 16qq .. +15 of its row (A: unit qq
+// of the activation row) and of its column (B: code words 2(qq%2), +1 of the
+// chunk lane (qq/2, column % 32)).  The MFMAs of row subtile i + 1 are issued
+// before subtile i is rescaled, so the matrix core and the vector unit
+// overlap; the copies of group g + 2 go out between subtiles.
+// The wave's weight-side operands of one group: int8 code fragments and the
+// scales of its two 16-column subtiles.  Every wave copies its own code and
+// scale chunk, so it may read them as soon as its own copies have landed,
+// before the barrier that publishes the activation rows copied by all waves.
+struct BState {
+  i32x4_t bq[kJJ];
+  float sc[kJJ];
+};
 
-  // activation staging: thread -> (row, half of the 64-byte group segment)
-  const int arow = tid >> 1;
-  const int ahalf = tid & 1;
-  int64_t src = row0 + min(arow, valid - 1);
-  if (a.x_rows) src = a.x_rows[src];
-  const uint4* aptr = reinterpret_cast<const uint4*>(a.xi + src * K + ahalf * 32);
-
-  const int ncol = nblk * kBN + wave * 64 + l32;
-  const int64_t c0 = (int64_t)e * a.N + ncol;
-  const int64_t c1 = c0 + 32;
-  const uint4* bp0 = reinterpret_cast<const uint4*>(a.w + c0 * KW) + h;
-  const uint4* bp1 = reinterpret_cast<const uint4*>(a.w + c1 * KW) + h;
-  const uint4* sp0 = reinterpret_cast<const uint4*>(a.s + c0 * G);
-  const uint4* sp1 = reinterpret_cast<const uint4*>(a.s + c1 * G);
-
-  f32x16_t acc[4][2];
+template <bool TILED>
+__device__ __forceinline__ BState load_bstate(const ICtx<TILED>& c, const char* st, int g) {
+  using C = ICfg<TILED>;
+  const int l16 = c.lane & 15, qq = c.lane >> 4;
+  BState b;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  uint4 areg[2];
-  uint4 braw[2];
-  uint4 sch[2];
-
-  auto stage_a = [&](int g, int buf) {
-    // 32 int8 per thread: store, and the exact row sum of the group (two threads per row)
-    int8_t* d = &As[buf][arow * kLDA + ahalf * 32];
-    reinterpret_cast<uint4*>(d)[0] = areg[0];
-    reinterpret_cast<uint4*>(d)[1] = areg[1];
-    int part = sum_i8x4(areg[0].x) + sum_i8x4(areg[0].y) + sum_i8x4(areg[0].z) + sum_i8x4(areg[0].w) +
-               sum_i8x4(areg[1].x) + sum_i8x4(areg[1].y) + sum_i8x4(areg[1].z) + sum_i8x4(areg[1].w);
-    part += __shfl_xor(part, 1, 64);
-    if (ahalf == 0) {
-      const float rf = (float)part;
-      const uint32_t hi = f32_to_bf16(rf);
-      const float lo = rf - bf16_to_f32(hi);  // exact: |R| <= 8128
-      Rhi[arow][g] = (uint16_t)hi;
-      Rlo[arow][g] = (uint16_t)f32_to_bf16(lo);
+  for (int jj = 0; jj < kJJ; ++jj) {
+    const int cc = 16 * jj + l16;  // column within the wave's 32
+    const uint2 wd = *reinterpret_cast<const uint2*>(st + C::kBOff + c.wave * 1024 + ((qq >> 1) * 32 + cc) * 16 +
+                                                     (qq & 1) * 8);
+    b.bq[jj] = codes_to_i8(wd.x, wd.y);
+    const int sc_i = 32 * (c.wave & 1) + cc;  // the column within its 64-column block
+    if constexpr (TILED) {
+      const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.wave * 256);
+      b.sc[jj] = __uint_as_float(sw[sc_i] << 16);
+    } else {
+      const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.wave * 512);
+      b.sc[jj] = __uint_as_float((sw[sc_i] << ((g & 1) ? 0 : 16)) & 0xFFFF0000u);
     }
-  };
+  }
+  return b;
+}
 
-  // prologue
-  areg[0] = aptr[0];
-  areg[1] = aptr[1];
-  braw[0] = bp0[0];
-  braw[1] = bp1[0];
-  sch[0] = sp0[0];
-  sch[1] = sp1[0];
-  stage_a(0, 0);
-  uint4 bcur[2] = {braw[0], braw[1]};
-  float scur[2] = {bf16_at(sch[0], 0), bf16_at(sch[1], 0)};
-
+// Main loop over the groups of one tile with MSUB 32-row subtiles.  Per group
+// and 16 x 16 subtile one v_mfma_i32_16x16x64_i8 covers the whole group;
+// lane quarter qq supplies group elements 16qq .. +15 of its row (A: unit qq
+// of the activation row) and of its column (B: code words 2(qq%2), +1 of the
+// chunk lane (qq/2, column % 32)).  The MFMAs of row subtile i + 1 are issued
+// before subtile i is rescaled, so the matrix core and the vector unit
+// overlap; the copies of group g + 2 go out between subtiles, and the next
+// group's code fragments and scales are read at the end of the iteration.
+template <bool TILED, int MSUB>
+__device__ __forceinline__ void tile_loop_i8(const ICtx<TILED>& c, char* smem, Acc& acc) {
+  using C = ICfg<TILED>;
+  constexpr int D = C::kCopies;
+  constexpr int NI = 2 * MSUB;  // 16-row subtiles
+  const int G = c.G;
+  const int l16 = c.lane & 15, qq = c.lane >> 4;
+  const int aoff = l16 * 64 + ((qq ^ aswz(l16)) * 16);  // the lane's A unit in row subtile 0
+  int16_t* rsum = reinterpret_cast<int16_t*>(smem + C::kRingBytes);
+  issue_group<TILED>(c, 0);
+  issue_group<TILED>(c, min(1, G - 1));
+  wait_vmem<D>();  // this wave's copies of group 0
+  BState bs = load_bstate<TILED>(c, smem, 0);
   for (int g = 0; g < G; ++g) {
-    const bool more = g + 1 < G;
-    if (more) {
-      const int gn = g + 1;
-      areg[0] = aptr[gn * 4];
-      areg[1] = aptr[gn * 4 + 1];
-      braw[0] = bp0[gn * 2];
-      braw[1] = bp1[gn * 2];
-      if ((gn & 7) == 0) {
-        sch[0] = sp0[gn >> 3];
-        sch[1] = sp1[gn >> 3];
+    // every wave's copies of group g have landed
+    __builtin_amdgcn_s_barrier();
+    const int cg = min(g + 2, G - 1);
+    const char* st = smem + (g % kStages) * C::kStageBytes;
+    const char* abuf = st + C::kAOff + aoff;
+    i32x4_t dc[kJJ], dn[kJJ];
+    {
+      const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf);
+#pragma unroll
+      for (int jj = 0; jj < kJJ; ++jj) {
+        const i32x4_t z = {};
+        dc[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bs.bq[jj], z, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      if (i + 1 < NI) {
+        const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf + (i + 1) * 16 * 64);
+#pragma unroll
+        for (int jj = 0; jj < kJJ; ++jj) {
+          const i32x4_t z = {};
+          dn[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bs.bq[jj], z, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < D; ++q)
+        if (q * NI / D == i) issue_copy<TILED>(c, cg, q);
+#pragma unroll
+      for (int jj = 0; jj < kJJ; ++jj) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][jj][r] = __builtin_fmaf(bs.sc[jj], (float)dc[jj][r], acc[i][jj][r]);
+        // keep the rescale here, between this subtile's and the next one's
+        // MFMAs, rather than sunk to the end of the group
+        asm volatile("" : "+v"(acc[i][jj]));
+      }
+#pragma unroll
+      for (int jj = 0; jj < kJJ; ++jj) dc[jj] = dn[jj];
+    }
+    // exact row sums of the group: wave w takes 16-row subtile w (16 int8 per
+    // lane, four lane quarters per row)
+    if (c.wave < NI) {
+      const int i = c.wave;
+      const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf + i * 16 * 64);
+      int part = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) part = __builtin_amdgcn_sdot4(af[t], 0x01010101, part, false);
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      if (qq == 0) rsum[g * kRStride + 16 * i + l16] = (int16_t)part;
+    }
+    // this wave's copies of group g + 1 (group g + 2's may be in flight)
+    wait_vmem<D>();
+    if (g + 1 < G) bs = load_bstate<TILED>(c, smem + ((g + 1) % kStages) * C::kStageBytes, g + 1);
+  }
+  wait_vmem<0>();  // the trailing repeat copies
+}
+
+// Bias term: acc += R (rows x groups) . b^T (groups x columns), bf16 MFMA
+// with R = hi + lo exact in bf16; then rows scaled by sx and stored.
+template <bool TILED>
+__device__ __forceinline__ void finish_tile(const Int8Args& a, char* smem, const ICtx<TILED>& c, Acc& acc, int e,
+                                            int64_t row0, int valid, int msub, int nblk) {
+  using C = ICfg<TILED>;
+  const int G = c.G;
+  const int l16 = c.lane & 15, qq = c.lane >> 4;
+  const int16_t* rsum = reinterpret_cast<const int16_t*>(smem + C::kRingBytes);
+  const float* sxl = reinterpret_cast<const float*>(smem + C::kRingBytes + C::kRBytes);
+  const int col0 = nblk * kBN + c.wave * kCols;
+  for (int g0 = 0; g0 < G; g0 += 32) {
+    // lane quarter qq supplies groups g0 + 8qq .. +7
+    i32x4_t bz[kJJ];
+#pragma unroll
+    for (int jj = 0; jj < kJJ; ++jj) {
+      const int n = col0 + 16 * jj + l16;
+      uint32_t v[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int g = g0 + 8 * qq + t;
+        uint32_t bits = 0;
+        if (g < G) {
+          if constexpr (TILED) {
+            const int64_t chunk = ((int64_t)e * (a.N / 64) + n / 64) * G + g;
+            bits = a.sb[chunk * 64 + (n & 63)] >> 16;
+          } else {
+            bits = a.b[((int64_t)e * a.N + n) * G + g];
+          }
+        }
+        v[t] = bits;
+      }
+      bz[jj] = i32x4_t{(int)(v[0] | (v[1] << 16)), (int)(v[2] | (v[3] << 16)), (int)(v[4] | (v[5] << 16)),
+                       (int)(v[6] | (v[7] << 16))};
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * kMaxSub; ++i) {
+      if (i >= 2 * msub) break;
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float f[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int g = g0 + 8 * qq + 2 * t + u;
+          f[u] = g < G ? (float)rsum[g * kRStride + 16 * i + l16] : 0.f;
+        }
+        const uint32_t hb = cvt_pk_bf16(f[0], f[1]);  // |R| < 2^13: hi = bf16(R), lo = R - hi exact
+        hi[t] = hb;
+        lo[t] = cvt_pk_bf16(f[0] - bf16lo(hb), f[1] - bf16hi(hb));
+      }
+      const i32x4_t ah = {(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      const i32x4_t al = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+#pragma unroll
+      for (int jj = 0; jj < kJJ; ++jj) {
+        acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ah),
+                                                             __builtin_bit_cast(bf16x8_t, bz[jj]), acc[i][jj], 0, 0, 0);
+        acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, al),
+                                                             __builtin_bit_cast(bf16x8_t, bz[jj]), acc[i][jj], 0, 0, 0);
+      }
+    }
+  }
+  // out = sx * acc through LDS, 64 rows per pass; staging row m holds the
+  // block's 256 columns (512 bytes), 16-byte unit u at u ^ (m & 31).
+  char* ep = smem;
+  const int tid = threadIdx.x;
+  uint16_t* obase = a.out + row0 * (int64_t)a.N + nblk * kBN;
+  for (int p = 0; 2 * p < msub; ++p) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2 * kMaxSub; ++i) {
+      if ((i >> 2) != p) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int mt = 16 * i + 4 * qq + r;  // row within the tile
+        const int m = mt - 64 * p;           // row within the pass
+        const float scale = sxl[mt];
+#pragma unroll
+        for (int jj = 0; jj < kJJ; ++jj) {
+          const int col = c.wave * kCols + 16 * jj + l16;  // column within the block
+          const int u = col >> 3;
+          *reinterpret_cast<uint16_t*>(ep + m * 512 + ((u ^ (m & 31)) * 16) + (col & 7) * 2) =
+              (uint16_t)(cvt_pk_bf16(scale * acc[i][jj][r], 0.f) & 0xFFFFu);
+        }
       }
     }
     __syncthreads();
-    const int8_t* abuf = As[g & 1];
-    i32x4_t bf[2][2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      bf[j][0] = codes_to_i8(bcur[j].x, bcur[j].y);
-      bf[j][1] = codes_to_i8(bcur[j].z, bcur[j].w);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i < msub) {
-        const i32x4_t a0 = *reinterpret_cast<const i32x4_t*>(abuf + (32 * i + l32) * kLDA + 32 * h);
-        const i32x4_t a1 = *reinterpret_cast<const i32x4_t*>(abuf + (32 * i + l32) * kLDA + 32 * h + 16);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          i32x16_t d = {};
-          d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bf[j][0], d, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bf[j][1], d, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(scur[j], (float)d[r], acc[i][j][r]);
-        }
-      }
-    }
-    if (more) {
-      stage_a(g + 1, (g + 1) & 1);
-      bcur[0] = braw[0];
-      bcur[1] = braw[1];
-      const int gi = (g + 1) & 7;
-      scur[0] = bf16_at(sch[0], gi);
-      scur[1] = bf16_at(sch[1], gi);
+    for (int it = 0; it < 64 * 32 / kI8Threads; ++it) {
+      const int m = it * (kI8Threads / 32) + tid / 32;
+      const int u = tid % 32;
+      const int row = 64 * p + m;
+      const uint4 v = *reinterpret_cast<const uint4*>(ep + m * 512 + ((u ^ (m & 31)) * 16));
+      if (row < valid) *reinterpret_cast<uint4*>(obase + (int64_t)row * a.N + u * 8) = v;
     }
   }
-  __syncthreads();
+}
 
-  // bias term: acc += R (rows x G) . b^T (G x cols), bf16 MFMA, R = hi + lo exactly
-  const uint4* zp0 = reinterpret_cast<const uint4*>(a.b + c0 * G);
-  const uint4* zp1 = reinterpret_cast<const uint4*>(a.b + c1 * G);
-  for (int g0 = 0; g0 < G; g0 += 16) {
-    // lane half h supplies g0 + 8h .. +7
-    const int gc = (g0 >> 3) + h;
-    const uint4 bz[2] = {zp0[gc], zp1[gc]};
+template <bool TILED>
+__device__ __forceinline__ void run_unit_i8(const Int8Args& a, char* smem, int tile, int nblk) {
+  using C = ICfg<TILED>;
+  const TileRows tr = tile_rows_of(Tiles{a.offsets, a.tile_row, a.tile_exp, a.ntiles, a.n_rows, a.num_experts}, tile);
+  if (tr.valid <= 0) return;
+  const int e = tr.e, valid = tr.valid;
+  const int64_t row0 = tr.row0;
+  const int msub = (valid + 31) / 32;
+  const int K = a.K;
+  const int G = K / 64;
+  const int tid = threadIdx.x;
+
+  ICtx<TILED> c;
+  c.G = G;
+  c.wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  c.lane = tid % 64;
+  c.l32 = c.lane % 32;
+  c.h = c.lane / 32;
+  c.lds = (uint32_t)(uintptr_t)smem;
+  // A copy q of wave w writes stage bytes (4q + w) * 1024 + lane * 16: row
+  // 16(4q + w) + lane/4, stored unit lane%4 holding logical unit
+  // (lane%4) ^ aswz(row).  Rows past the tile repeat its last row.
+  float* sxl = reinterpret_cast<float*>(smem + C::kRingBytes + C::kRBytes);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i < msub) {
-        const i32x4_t rh = *reinterpret_cast<const i32x4_t*>(&Rhi[32 * i + l32][g0 + 8 * h]);
-        const i32x4_t rl = *reinterpret_cast<const i32x4_t*>(&Rlo[32 * i + l32][g0 + 8 * h]);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const bf16x8_t bb = __builtin_bit_cast(bf16x8_t, bz[j]);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, rh), bb, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, rl), bb, acc[i][j], 0, 0, 0);
-        }
-      }
-    }
+  for (int q = 0; q < C::kACopies; ++q) {
+    const int row = 16 * (q * kWaves + c.wave) + (c.lane >> 2);
+    const int unit = (c.lane & 3) ^ aswz(row);
+    int64_t src = row0 + min(row, valid - 1);
+    if (a.x_rows) src = a.x_rows[src];
+    c.a_src[q] = reinterpret_cast<const char*>(a.xi + src * K + unit * 16);
+  }
+  if (tid < kBM) {
+    int64_t src = row0 + min(tid, valid - 1);
+    if (a.x_rows) src = a.x_rows[src];
+    sxl[tid] = a.sx[src];
+  }
+  // the wave's 32 columns: half (wave & 1) of the 64-column block nblk * 4 + wave / 2
+  const int c64 = nblk * (kBN / 64) + c.wave / 2;
+  if constexpr (TILED) {
+    const int64_t chunk0 = ((int64_t)e * (a.N / 64) + c64) * G;
+    c.b_src = reinterpret_cast<const char*>(a.w) + (chunk0 * 2 + (c.wave & 1)) * 1024 + c.lane * 16;
+    c.s_src = reinterpret_cast<const char*>(a.sb) + chunk0 * 256 + c.lane * 4;
+    c.z_src = nullptr;
+  } else {
+    const int64_t KW = K / 8;
+    const int64_t col64 = (int64_t)e * a.N + c64 * 64;
+    c.b_src = reinterpret_cast<const char*>(a.w + (col64 + 32 * (c.wave & 1) + c.l32) * KW + c.h * 4);
+    c.s_src = reinterpret_cast<const char*>(a.s + (col64 + c.lane) * G);
+    c.z_src = reinterpret_cast<const char*>(a.b + (col64 + c.lane) * G);
   }
 
+  Acc acc;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (i >= msub) continue;
+  for (int i = 0; i < 2 * kMaxSub; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-      if (m < valid) {
-        int64_t xr = row0 + m;
-        const float scale = a.sx[a.x_rows ? (int64_t)a.x_rows[xr] : xr];
-        uint16_t* orow = a.out + (row0 + m) * (int64_t)a.N + ncol;
-        orow[0] = (uint16_t)f32_to_bf16(scale * acc[i][0][r]);
-        orow[32] = (uint16_t)f32_to_bf16(scale * acc[i][1][r]);
-      }
-    }
+    for (int j = 0; j < kJJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
+
+  switch (msub) {
+    case 1: tile_loop_i8<TILED, 1>(c, smem, acc); break;
+    case 2: tile_loop_i8<TILED, 2>(c, smem, acc); break;
+    case 3: tile_loop_i8<TILED, 3>(c, smem, acc); break;
+    default: tile_loop_i8<TILED, 4>(c, smem, acc); break;
   }
+  __syncthreads();  // row sums and sx visible to every wave; the ring is free
+  finish_tile<TILED>(a, smem, c, acc, e, row0, valid, msub, nblk);
+}
+
+template <bool TILED>
+__global__ __launch_bounds__(kI8Threads, kI8BlocksPerCU) void gemm_int8_kernel(Int8Args a) {
+  using C = ICfg<TILED>;
+  __shared__ __attribute__((aligned(1024))) char smem[C::kLdsBytes];
+  __shared__ int order[kMaxOrder];
+
+  const Tiles tt{a.offsets, a.tile_row, a.tile_exp, a.ntiles, a.n_rows, a.num_experts};
+  const int NB = a.N / kBN;
+  const int ntiles = a.ntiles[0];
+  const Snake sn((int64_t)ntiles * NB);
+  if (sn.unit(0) < 0) return;
+  const bool sorted = ntiles <= kMaxOrder;
+  if (sorted) rank_tiles(tt, ntiles, order, reinterpret_cast<int*>(smem));
+  for (int64_t k = 0;; ++k) {
+    const int64_t u = sn.unit(k);
+    if (u < 0) break;
+    const int rank = (int)(u / NB);
+    __syncthreads();  // every wave is done with the ring and the row sums
+    run_unit_i8<TILED>(a, smem, sorted ? order[rank] : rank, (int)(u % NB));
+  }
+}
+
+int launch_int8(const Int8Args& a, int64_t max_tiles, void* stream) {
+  const dim3 grid((unsigned)grid_blocks(max_tiles * (a.N / kBN), kI8BlocksPerCU));
+  hipStream_t st = qmoe::as_stream(stream);
+  if (a.sb) gemm_int8_kernel<true><<<grid, dim3(kI8Threads), 0, st>>>(a);
+  else gemm_int8_kernel<false><<<grid, dim3(kI8Threads), 0, st>>>(a);
+  return qmoe::launch_status("gemm_int8_kernel");
+}
+
+int check_int8(const int8_t* xi, const float* sx, int64_t n_rows, int64_t K, int32_t num_experts, int64_t N,
+               const int32_t* offsets, const int32_t* tile_row, const int32_t* tile_exp, const int32_t* ntiles,
+               int64_t max_tiles, const uint16_t* out) {
+  if (n_rows < 0 || K <= 0 || N <= 0 || num_experts <= 0 || max_tiles < 0)
+    return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (n_rows == 0 || max_tiles == 0) return QMOE_OK;
+  if (!xi || !sx || !offsets || !tile_row || !tile_exp || !ntiles || !out)
+    return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (K % 64 || K > 64 * kMaxG)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 64, at most %d", (long long)K, 64 * kMaxG);
+  if (N % kBN) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of %d", (long long)N, kBN);
+  if (!qmoe::aligned16(xi) || !qmoe::aligned16(out)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "xi and out must be 16-byte aligned");
+  if (N > 0x7FFFFFFF || n_rows > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
+  return QMOE_OK;
 }
 
 }  // namespace
@@ -300,26 +551,33 @@ extern "C" int qmoe_gather_qmm_int8_sorted(const int8_t* xi, const float* sx, co
                                            int bits, const int32_t* offsets, const int32_t* tile_row,
                                            const int32_t* tile_exp, const int32_t* ntiles, int64_t max_tiles,
                                            uint16_t* out, void* stream) {
-  if (n_rows < 0 || K <= 0 || N <= 0 || num_experts <= 0 || max_tiles < 0)
-    return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
-  if (n_rows == 0 || max_tiles == 0) return QMOE_OK;
-  if (!xi || !sx || !w || !scales || !biases || !offsets || !tile_row || !tile_exp || !ntiles || !out)
-    return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  const int rc = check_int8(xi, sx, n_rows, K, num_experts, N, offsets, tile_row, tile_exp, ntiles, max_tiles, out);
+  if (rc != QMOE_OK || n_rows == 0 || max_tiles == 0) return rc;
+  if (!w || !scales || !biases) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
   if (bits != 4 || group_size != 64)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "int8 GEMM takes 4-bit codes with group_size 64 (got %d, %d)", bits,
                       group_size);
-  if (K % 1024 || K > 64 * kMaxG)
-    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 1024, at most %d", (long long)K,
-                      64 * kMaxG);
-  if (N % kBN) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of %d", (long long)N, kBN);
-  if (!qmoe::aligned16(xi) || !qmoe::aligned16(w) || !qmoe::aligned16(scales) || !qmoe::aligned16(biases))
-    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "xi, w, scales and biases must be 16-byte aligned");
-  if (N > 0x7FFFFFFF || n_rows > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
-  if (qmoe_gemm_tile_rows() != kTileRows) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "tile rows mismatch");
-  const int64_t blocks = max_tiles * (kTileRows / kBM) * (N / kBN);
-  if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
-  Int8Args a{xi, sx, x_rows, n_rows, (int)K, w, scales, biases, num_experts, (int)N, offsets, tile_row, tile_exp,
-             ntiles, out};
-  gemm_int8_kernel<<<dim3((unsigned)blocks), dim3(kThreads), 0, qmoe::as_stream(stream)>>>(a);
-  return qmoe::launch_status("gemm_int8_kernel");
+  // scales and biases are copied in pairs of groups
+  if (K % 128) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 128", (long long)K);
+  if (!qmoe::aligned16(w) || !qmoe::aligned16(scales) || !qmoe::aligned16(biases))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "w, scales and biases must be 16-byte aligned");
+  Int8Args a{xi, sx, x_rows, n_rows, (int)K, w, scales, biases, nullptr, num_experts, (int)N, offsets, tile_row,
+             tile_exp, ntiles, out};
+  return launch_int8(a, max_tiles, stream);
+}
+
+extern "C" int qmoe_gather_qmm_int8_sorted_tiles(const int8_t* xi, const float* sx, const int32_t* x_rows,
+                                                 int64_t n_rows, int64_t K, const uint32_t* wp, const uint32_t* sb,
+                                                 int32_t num_experts, int64_t N, const int32_t* offsets,
+                                                 const int32_t* tile_row, const int32_t* tile_exp,
+                                                 const int32_t* ntiles, int64_t max_tiles, uint16_t* out,
+                                                 void* stream) {
+  const int rc = check_int8(xi, sx, n_rows, K, num_experts, N, offsets, tile_row, tile_exp, ntiles, max_tiles, out);
+  if (rc != QMOE_OK || n_rows == 0 || max_tiles == 0) return rc;
+  if (!wp || !sb) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (!qmoe::aligned16(wp) || !qmoe::aligned16(sb))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "wp and sb must be 16-byte aligned");
+  Int8Args a{xi, sx, x_rows, n_rows, (int)K, wp, nullptr, nullptr, sb, num_experts, (int)N, offsets, tile_row,
+             tile_exp, ntiles, out};
+  return launch_int8(a, max_tiles, stream);
 }

@@ -529,9 +529,31 @@ def gather_qmm_int8_sorted(xi: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, 
     return out
 
 
+def gather_qmm_int8_sorted_tiles(xi: torch.Tensor, sx: torch.Tensor, tw: TileWeights, tiles: TileTable,
+                                 x_rows: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`gather_qmm_int8_sorted` over tile-layout weights; same result."""
+    _dev(xi, "xi")
+    if xi.dtype != torch.int8:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"xi must be int8, got {xi.dtype}")
+    xi = _ready(xi)
+    sx = _f32(sx, "sx", xi.device)
+    K = xi.shape[-1]
+    if K != tw.K:
+        raise ValueError(f"x has K={K}, the weights K={tw.K}")
+    xr = None if x_rows is None else _i32(x_rows.reshape(-1), "x_rows", xi.device)
+    if tiles.num_experts != tw.num_experts or tiles.tile_rows != tile_rows():
+        raise ValueError("tile table does not match this call")
+    out = torch.empty(tiles.rows, tw.N, dtype=torch.bfloat16, device=xi.device)
+    _lib.call("qmoe_gather_qmm_int8_sorted_tiles", xi.data_ptr(), sx.data_ptr(), _ptr(xr), tiles.rows, K,
+              tw.wp.data_ptr(), tw.sb.data_ptr(), tw.num_experts, tw.N, tiles.offsets.data_ptr(),
+              tiles.tile_row.data_ptr(), tiles.tile_exp.data_ptr(), tiles.ntiles.data_ptr(), tiles.maxt,
+              out.data_ptr(), _stream(xi))
+    return out
+
+
 __all__ = [
     "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "TileWeights", "Routing", "build_tiles", "route",
-    "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmv_tiles", "gate_up_silu_tiles",
+    "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmm_int8_sorted_tiles", "gather_qmv_tiles", "gate_up_silu_tiles",
     "max_tiles", "tile_rows", "unpack", "dequantize", "gather_qmv", "gather_qmm_sorted", "gather_qmm",
     "gemm_supported", "quantized_matmul", "gate_up_silu", "down_wsum", "moe_weighted_sum",
     "quantize_act_int8", "gather_qmm_int8_sorted",
