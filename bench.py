@@ -143,7 +143,7 @@ def calibration_copy(dev, mib=CALIBRATION_MIB, reps=5):
 # `--traffic` measures them live (rocprofv3 children started before this
 # process touches the GPU); otherwise the committed summary supplies them.
 
-TRAFFIC_KERNEL = "qmv64_kernel<1, 1, 4>"
+TRAFFIC_KERNEL = "qmv64_kernel<1, 1, 4, 64, true, false>"  # the decode gate_up + SwiGLU kernel (bench workload 1)
 TRAFFIC_PROFILE = ROOT / "profiles" / "qmv64_decode_gate_up.traffic.txt"
 
 
@@ -313,7 +313,7 @@ def setup_cfg1(args, dev):
 
     return wl, [mk_mlx(i) for i in range(args.steps)], {
         "bytes": synth.algorithmic_bytes(1), "flops": synth.algorithmic_flops(1), "bound": "hbm",
-        "kernel": "qmv64_kernel<1,1,4>", "sets": len(sets),
+        "kernel": "qmv64_kernel<1, 1, 4, 64, true, false>", "sets": len(sets),
         "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(args.steps)]),
         "workload": "decode gate_up gather_qmm + SwiGLU: 1 token, H=2048, E=256, top_k=10, "
                     "W [256,1024,2048] int4 g64 bf16 scale/bias -> h [10,512]"}
@@ -348,7 +348,7 @@ def setup_cfg0(args, dev):
 
     return wl, [mk_mlx(i) for i in range(args.steps)], {
         "bytes": synth.algorithmic_bytes(0), "flops": synth.algorithmic_flops(0), "bound": "hbm",
-        "kernel": "qmv64_kernel<1,0,2>", "sets": len(sets),
+        "kernel": "qmv64_kernel<1, 0, 2, 64, false, false>", "sets": len(sets),
         "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(args.steps)]),
         "workload": "dense quantized_matmul x [1,2048] . W [4096,2048] int4 g64"}
 

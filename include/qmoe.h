@@ -258,6 +258,34 @@ int qmoe_gather_qmm_int8_sorted_tiles(const int8_t* xi, const float* sx,
                                       const int32_t* ntiles, int64_t max_tiles,
                                       uint16_t* out, void* stream);
 
+/* gate_up grouped GEMM with the SwiGLU epilogue fused: weights [E, N = 2I, K]
+ * in the tile layout of the gate/up-PAIRED row order (row 64c + j of the
+ * paired order is gate row 32c + j for j < 32 and up row I + 32c + j - 32
+ * otherwise; ops.repack_tiles(..., swiglu_pairs=True)), output
+ * h [n_rows, I] bf16 = silu(gate) * up from the fp32 accumulators, rounded
+ * once.  Replaces SwitchGLU's gate_up gather, split and activation
+ * (switch_layers.py:213-237) for the sorted prefill form; N % 256 == 0. */
+int qmoe_gather_qmm_swiglu_sorted_tiles(const uint16_t* x, const int32_t* x_rows,
+                                        int64_t n_rows, int64_t K,
+                                        const uint32_t* wp, const uint32_t* sb,
+                                        int32_t num_experts, int64_t N,
+                                        const int32_t* offsets,
+                                        const int32_t* tile_row,
+                                        const int32_t* tile_exp,
+                                        const int32_t* ntiles, int64_t max_tiles,
+                                        uint16_t* h, void* stream);
+
+/* ---------------------------------------------------------------- router --
+ * Top-k experts per token from fp32 router logits [T, E] (replaces the
+ * reference's fused router_topk, engine/patches/decode-fusion/
+ * fused_kernels.py:363-371, and the stock softmax / argpartition / take /
+ * renormalise of qwen3_5_moe/language.py:65-71): idx[t, j] the j-th largest
+ * logit's expert (descending, ties to the lower index), scores[t, j] fp32:
+ * norm != 0: exp(l_j - l_0) / sum_{j<k} exp(l_j - l_0); norm == 0: the full
+ * softmax probability.  k <= 64, E <= 1024; logits are expected finite. */
+int qmoe_router_topk(const float* logits, int64_t T, int64_t E, int64_t k,
+                     int norm, int32_t* idx, float* scores, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,7 @@ def lib():
         L.orc_quant_act_int8.argtypes = [P, I64, I64, P, P]
         L.orc_gather_qmm_int8_rows.argtypes = [P, P, I64, P, P, I64, P, P, P, I64,
                                                INT, INT, P, P, INT]
+        L.orc_router_topk.argtypes = [P, I64, I64, I64, INT, P, P]
         L.orc_max_threads.restype = INT
         _lib = L
     return _lib
@@ -224,6 +225,17 @@ def down_wsum(h, idx, scores, w, s, b, group_size=64, bits=4, n_threads=0):
     lib().orc_down_wsum(_p(h), _p(idx), _p(scores), T, k, I, _p(w), _p(s), _p(b), D,
                         group_size, bits, _p(y64), _p(y16), n_threads)
     return y64, y16
+
+
+def router_topk(logits, k: int, norm: bool = True):
+    """Top-k experts per token by fp32 logit (ties to the lower index),
+    descending; scores in float64 (fused_kernels.py:363-371)."""
+    lg = _c(logits, np.float32)
+    T, E = lg.reshape(-1, lg.shape[-1]).shape
+    idx = np.empty((T, k), np.int32)
+    sc = np.empty((T, k), np.float64)
+    lib().orc_router_topk(_p(lg), T, E, k, int(norm), _p(idx), _p(sc))
+    return idx, sc
 
 
 def quant_act_int8(x):

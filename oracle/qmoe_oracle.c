@@ -404,3 +404,34 @@ int orc_max_threads(void) {
   return 1;
 #endif
 }
+
+/* -------------------------------------------------------------- router */
+
+/* fused_kernels.py:288-330: k rounds of (max value, lowest index holding it). */
+void orc_router_topk(const float* logits, int64_t T, int64_t E, int64_t k, int norm,
+                     int32_t* idx, double* scores) {
+  for (int64_t t = 0; t < T; ++t) {
+    const float* l = logits + t * E;
+    unsigned char* taken = (unsigned char*)calloc((size_t)E, 1);
+    double lmax = -INFINITY;
+    for (int64_t e = 0; e < E; ++e) if ((double)l[e] > lmax) lmax = l[e];
+    double all = 0.0;
+    for (int64_t e = 0; e < E; ++e) all += exp((double)l[e] - lmax);
+    for (int64_t j = 0; j < k; ++j) {
+      int64_t best = -1;
+      for (int64_t e = 0; e < E; ++e)
+        if (!taken[e] && (best < 0 || l[e] > l[best])) best = e;
+      taken[best] = 1;
+      idx[t * k + j] = (int32_t)best;
+    }
+    if (norm) {
+      const double l0 = l[idx[t * k]];
+      double sum = 0.0;
+      for (int64_t j = 0; j < k; ++j) sum += exp((double)l[idx[t * k + j]] - l0);
+      for (int64_t j = 0; j < k; ++j) scores[t * k + j] = exp((double)l[idx[t * k + j]] - l0) / sum;
+    } else {
+      for (int64_t j = 0; j < k; ++j) scores[t * k + j] = exp((double)l[idx[t * k + j]] - lmax) / all;
+    }
+    free(taken);
+  }
+}

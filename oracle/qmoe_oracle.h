@@ -109,6 +109,15 @@ void orc_gather_qmm_int8_rows(const int8_t* xi, const float* sx, int64_t K,
                               int group_size, int bits, double* out_f64,
                               uint16_t* out_bf16, int n_threads);
 
+/* a14: fused router top-k (engine/patches/decode-fusion/fused_kernels.py:363-371
+ * router_topk, kernel source :288-330).  Per token the k largest logits in
+ * descending order, ties to the lower expert index; scores in double:
+ * norm != 0: exp(l_j - l_0) / sum_{j<k} exp(l_j - l_0) (the softmax over
+ * all experts renormalised over the chosen k, language.py:65-71);
+ * norm == 0: exp(l_j - max) / sum_all exp(l - max). */
+void orc_router_topk(const float* logits, int64_t T, int64_t E, int64_t k, int norm,
+                     int32_t* idx, double* scores);
+
 /* Number of OpenMP threads the oracle would use (for the CPU baseline). */
 int orc_max_threads(void);
 

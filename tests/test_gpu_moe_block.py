@@ -1,0 +1,163 @@
+"""The router top-k kernel, the SwiGLU-epilogue grouped GEMM and the whole
+routed MoE block (titan_amd.moe_block) against the CPU oracle.
+
+Bars: router indices exact (ties to the lower index) and scores within fp32
+rounding of the float64 oracle; h and the block output within 1 bf16 ULP of
+the fp64 golden chain on live elements (the rule of the other parity tests),
+with the weights exact for the decode kernels and bf16-materialised for the
+grouped GEMMs (the MLX qmv / qmm split).
+The block is checked stage by stage: its expert selection against the oracle
+on the GPU's own fp32 logits, then its output against an oracle chain that
+takes the same selection, so a near-tie in routing cannot mask or fake an
+arithmetic error.  The shared-expert branch adds two bf16 roundings (its
+gated output, then the sum with the routed output) and is held to 2^-7 of
+max|y| against the fp64 chain.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close_bf16, bf16_t, bits, f32_t, words_t
+from titan_amd import moe_block, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 256, 10), (4096, 256, 10), (7, 512, 8), (5, 100, 6), (3, 64, 64)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_router_topk_matches_oracle(dev, orc, T, E, k, norm):
+    say(f"router top-k T={T} E={E} k={k} norm={norm}")
+    rng = np.random.default_rng(T + E + k)
+    lg = (rng.normal(size=(T, E)) * 2).astype(np.float32)
+    idx, sc = ops.router_topk(f32_t(lg, dev), k, norm)
+    ridx, rsc = orc.router_topk(lg, k, norm)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
+
+
+def test_router_topk_ties_take_lower_index(dev, orc):
+    say("router top-k ties")
+    lg = np.zeros((3, 256), np.float32)
+    lg[0, [3, 70, 9]] = 1.0
+    lg[1, :] = 0.5
+    lg[2, 200:] = 2.0
+    idx, sc = ops.router_topk(f32_t(lg, dev), 10, True)
+    ridx, rsc = orc.router_topk(lg, 10, True)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert idx[0, :4].tolist() == [3, 9, 70, 0]
+    np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("E,I,K,counts", [
+    (4, 512, 2048, [1, 129, 300, 64]),
+    (8, 128, 1024, [7, 0, 33, 97, 128, 200, 2, 65]),
+    (3, 256, 512, [256, 5, 100]),
+])
+def test_swiglu_gemm_matches_oracle(dev, orc, E, I, K, counts):
+    say(f"SwiGLU grouped GEMM E={E} I={I} K={K}")
+    rng = np.random.default_rng(E * I + K)
+    w, s, b = synth.quant_weights(rng, (E, 2 * I), K)
+    ids = np.repeat(np.arange(E), counts).astype(np.int32)
+    x = synth.bf16_bits(rng.normal(size=(len(ids), K)).astype(np.float32))
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), swiglu_pairs=True)
+    tiles = ops.build_tiles(torch.from_numpy(ids).to(dev), E)
+    h = ops.gather_qmm_swiglu_sorted_tiles(bf16_t(x, dev), tw, tiles)
+    gu64, _ = orc.gather_qmm_rows(x, None, ids, w, s, b, deq="bf16")  # the GEMM's bf16 weights
+    h64, _ = orc.swiglu(gu64)
+    assert_close_bf16(orc, bits(h), h64, what=f"swiglu gemm {E}/{I}/{K}")
+
+
+def _block_problem(seed, E, H, I, with_shared=False):
+    rng = np.random.default_rng(seed)
+    gu = synth.quant_weights(rng, (E, 2 * I), H)
+    dn = synth.quant_weights(rng, (E, H), I)
+    router = synth.bf16_bits((rng.normal(size=(E, H)) * 0.05).astype(np.float32))
+    shared = None
+    if with_shared:
+        sgu = synth.quant_weights(rng, (1, 2 * I), H)
+        sdn = synth.quant_weights(rng, (1, H), I)
+        sg = synth.bf16_bits((rng.normal(size=(1, H)) * 0.05).astype(np.float32))
+        shared = (sgu, sdn, sg)
+    return gu, dn, router, shared
+
+
+def _dev_w(t, dev):
+    w, s, b = t
+    return words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev)
+
+
+@pytest.mark.parametrize("T", [1, 3, 6, 7, 300])
+def test_moe_block_matches_oracle_chain(dev, orc, T):
+    E, H, I, k = 64, 2048, 512, 10
+    say(f"MoE block T={T} E={E} H={H} I={I} k={k}")
+    gu, dn, router, _ = _block_problem(T + 5, E, H, I)
+    rng = np.random.default_rng(T)
+    x = synth.bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
+    blk = moe_block.SparseMoeBlock(bf16_t(router, dev), _dev_w(gu, dev), _dev_w(dn, dev), k)
+    xt = bf16_t(x, dev)
+    y = bits(blk(xt))
+    # stage 1: the selection, on the block's own fp32 logits
+    logits = torch.matmul(xt.float(), bf16_t(router, dev).float().t()).cpu().numpy()
+    idx, sc = blk.route(xt)
+    ridx, rsc = orc.router_topk(logits, k, True)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
+    sc32 = sc.cpu().numpy()
+    if T * k < moe_block.DECODE_MAX_PAIRS:
+        # stage 2: h = silu(gate) * up per (token, slot); stage 3: the fused
+        # down + weighted sum, the oracle fed the kernel's own h
+        h = ops.gate_up_silu(xt, *blk.gate_up, idx)
+        tok = np.repeat(np.arange(T), k).astype(np.int32)
+        gu64, _ = orc.gather_qmm_rows(x, tok, ridx.reshape(-1), *gu)
+        h64, _ = orc.swiglu(gu64)
+        assert_close_bf16(orc, bits(h).reshape(T * k, I), h64, what=f"block h T={T}")
+        y64, _ = orc.down_wsum(bits(h), ridx, sc32, *dn)
+        assert_close_bf16(orc, y, y64, what=f"block y T={T}")
+        want = bits(ops.down_wsum(h, *blk.down, idx, sc))
+    else:
+        # stage 2: routing sort + SwiGLU gate_up GEMM; stage 3: down GEMM on
+        # the kernel's own h; stage 4: un-permute + weighted sum, bit-exact
+        r = ops.route(idx, E)
+        order = r.order.cpu().numpy()
+        srt = r.sorted_ids.cpu().numpy()
+        assert np.array_equal(srt, ridx.reshape(-1)[order])
+        lhs = torch.div(r.order, k, rounding_mode="floor").to(torch.int32)
+        h = ops.gather_qmm_swiglu_sorted_tiles(xt, blk.gu_tiles, r.tiles, x_rows=lhs)
+        gu64, _ = orc.gather_qmm_rows(x, order // k, srt, *gu, deq="bf16")
+        h64, _ = orc.swiglu(gu64)
+        assert_close_bf16(orc, bits(h), h64, what=f"block h T={T}")
+        yd = ops.gather_qmm_sorted_tiles(h, blk.down_tiles, r.tiles)
+        yd64, _ = orc.gather_qmm_rows(bits(h), None, srt, *dn, deq="bf16")
+        assert_close_bf16(orc, bits(yd), yd64, what=f"block down T={T}")
+        want = orc.weighted_sum(bits(yd), r.inv_order.cpu().numpy(), sc32, T, k, H, blk.wsum_mode)
+    assert np.array_equal(y, want), f"block output differs from its stages (T={T})"
+
+
+@pytest.mark.parametrize("T", [2, 200])
+def test_moe_block_shared_expert(dev, orc, T):
+    E, H, I, k = 32, 2048, 512, 4
+    say(f"MoE block with shared expert T={T}")
+    gu, dn, router, (sgu, sdn, sg) = _block_problem(T + 9, E, H, I, with_shared=True)
+    rng = np.random.default_rng(T + 1)
+    x = synth.bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
+    shared = moe_block.SharedExpert(_dev_w(sgu, dev), _dev_w(sdn, dev), bf16_t(sg, dev))
+    blk = moe_block.SparseMoeBlock(bf16_t(router, dev), _dev_w(gu, dev), _dev_w(dn, dev), k, shared=shared)
+    xt = bf16_t(x, dev)
+    y = blk(xt).float().cpu().numpy()
+    routed = blk.experts(xt, *blk.route(xt)).float().cpu().numpy()
+    # shared branch: the oracle's dense SwiGLU MLP on the same x, gated
+    zero = np.zeros(T, np.int32)
+    deq = "exact" if T <= 16 else "bf16"  # decode kernels vs the GEMMs
+    gu64, _ = orc.gather_qmm_rows(x, None, zero, *sgu, deq=deq)
+    _, h16 = orc.swiglu(gu64)
+    sh64, _ = orc.gather_qmm_rows(h16, None, zero, *sdn, deq=deq)
+    g = 1.0 / (1.0 + np.exp(-(orc.f32_from_bf16(x).astype(np.float64) @ orc.f32_from_bf16(sg)[0].astype(np.float64))))
+    want = routed.astype(np.float64) + g[:, None] * sh64
+    err = np.abs(y - want).max() / np.abs(want).max()
+    print(f"[parity] shared block rel_to_max {err:.3g}", flush=True)
+    assert err <= 2.0 ** -7

@@ -69,6 +69,8 @@ SIGNATURES: dict[str, tuple] = {
     "qmoe_gather_qmm_int8_sorted": (INT, [P, P, P, I64, I64, P, P, P, I32, I64, INT, INT, P, P, P, P,
                                           I64, P, P]),
     "qmoe_gather_qmm_int8_sorted_tiles": (INT, [P, P, P, I64, I64, P, P, I32, I64, P, P, P, P, I64, P, P]),
+    "qmoe_router_topk": (INT, [P, I64, I64, I64, INT, P, P, P]),
+    "qmoe_gather_qmm_swiglu_sorted_tiles": (INT, [P, P, I64, I64, P, P, I32, I64, P, P, P, P, I64, P, P]),
 }
 
 _lock = threading.Lock()

@@ -312,7 +312,55 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, char* smem, const 
   }
 }
 
+// SwiGLU epilogue over gate/up-paired weights (qmoe_repack_tiles of the
+// paired row order): subtile j = 0 of a wave holds gate rows and j = 1 the
+// up rows of the same 32 intermediate indices, so every lane has both
+// operands of its h elements: h = silu(gate) * up in fp32 from the
+// accumulators (switch_layers.py:229-237, activations.py:9-11), rounded once
+// to bf16.  The block's 128 h columns leave through LDS as 256-byte row
+// segments, 16-byte unit u of staging row m at u ^ (m & 15).
 template <bool TILED>
+__device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, char* smem, const Ctx<TILED>& c,
+                                                  const f32x16_t (&acc)[kMaxSub][2], int64_t row0, int valid,
+                                                  int msub, int nblk) {
+  constexpr int kPassRows = 64;
+  constexpr int kHBlock = kBN / 2;  // h columns per block
+  const int NH = a.N / 2;
+  char* ep = smem;
+  const int tid = threadIdx.x;
+  uint16_t* obase = a.out + row0 * (int64_t)NH + nblk * kHBlock;
+  for (int p = 0; 2 * p < msub; ++p) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kMaxSub; ++i) {
+      if ((i >> 1) != p) continue;
+      const int m = 32 * (i & 1) + c.l32;  // row within the pass
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float hv[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float g = acc[i][0][4 * q + t], u = acc[i][1][4 * q + t];
+          hv[t] = g / (1.0f + __expf(-g)) * u;
+        }
+        const int gi = (c.wave * 32 + 8 * q + 4 * c.h) / 4;  // 8-byte granule within the 256-byte row
+        const uint2 v = make_uint2(cvt_pk_bf16(hv[0], hv[1]), cvt_pk_bf16(hv[2], hv[3]));
+        *reinterpret_cast<uint2*>(ep + m * 256 + ((((gi >> 1) ^ (m & 15)) << 1) | (gi & 1)) * 8) = v;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kPassRows * 16 / kThreads; ++it) {
+      const int m = it * (kThreads / 16) + tid / 16;
+      const int u = tid % 16;
+      const int row = kPassRows * p + m;
+      const uint4 v = *reinterpret_cast<const uint4*>(ep + m * 256 + ((u ^ (m & 15)) * 16));
+      if (row < valid) *reinterpret_cast<uint4*>(obase + (int64_t)row * NH + u * 8) = v;
+    }
+  }
+}
+
+template <bool TILED, bool SWIGLU>
 __device__ __forceinline__ void run_unit(const GemmArgs& a, char* smem, int tile, int nblk) {
   const TileRows tr = tile_rows_of(Tiles{a.offsets, a.tile_row, a.tile_exp, a.ntiles, a.n_rows, a.num_experts}, tile);
   const int e = tr.e, valid = tr.valid;
@@ -387,12 +435,13 @@ __device__ __forceinline__ void run_unit(const GemmArgs& a, char* smem, int tile
   // a row-major staging area (16-byte unit u of row m at u ^ (m & 31), which
   // keeps both the quad writes and the 16-byte row reads spread over the
   // banks), then the block stores the rows.
-  store_tile<TILED>(a, smem, c, acc, row0, valid, msub, nblk);
+  if constexpr (SWIGLU) store_tile_swiglu<TILED>(a, smem, c, acc, row0, valid, msub, nblk);
+  else store_tile<TILED>(a, smem, c, acc, row0, valid, msub, nblk);
 }
 
 // Persistent grid (kBlocksPerCU blocks per CU), each block walking its
 // slot's units of the ranked tile order.
-template <bool TILED>
+template <bool TILED, bool SWIGLU>
 __global__ __launch_bounds__(kThreads, kBlocksPerCU) void gemm_bf16_kernel(GemmArgs a) {
   using C = Cfg<TILED>;
   __shared__ __attribute__((aligned(1024))) char smem[C::kLdsBytes];
@@ -410,7 +459,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void gemm_bf16_kernel(GemmA
     if (u < 0) break;
     const int rank = (int)(u / NB);
     __syncthreads();  // every wave is done with the ring before it is refilled
-    run_unit<TILED>(a, smem, sorted ? order[rank] : rank, (int)(u % NB));
+    run_unit<TILED, SWIGLU>(a, smem, sorted ? order[rank] : rank, (int)(u % NB));
   }
 }
 
@@ -420,11 +469,12 @@ extern "C" int qmoe_gemm_tile_rows(void) { return kBM; }
 
 namespace {
 
-int launch_gemm(const GemmArgs& a, int64_t max_tiles, bool tiled, void* stream) {
+int launch_gemm(const GemmArgs& a, int64_t max_tiles, bool tiled, void* stream, bool swiglu = false) {
   const dim3 grid((unsigned)grid_blocks(max_tiles * (a.N / kBN)));
   hipStream_t st = qmoe::as_stream(stream);
-  if (tiled) gemm_bf16_kernel<true><<<grid, dim3(kThreads), 0, st>>>(a);
-  else gemm_bf16_kernel<false><<<grid, dim3(kThreads), 0, st>>>(a);
+  if (swiglu) gemm_bf16_kernel<true, true><<<grid, dim3(kThreads), 0, st>>>(a);
+  else if (tiled) gemm_bf16_kernel<true, false><<<grid, dim3(kThreads), 0, st>>>(a);
+  else gemm_bf16_kernel<false, false><<<grid, dim3(kThreads), 0, st>>>(a);
   return qmoe::launch_status("gemm_bf16_kernel");
 }
 
@@ -480,6 +530,23 @@ extern "C" int qmoe_gather_qmm_sorted_tiles(const uint16_t* x, const int32_t* x_
   GemmArgs a{x, x_rows, n_rows, (int)K, wp, nullptr, nullptr, sb, num_experts, (int)N, offsets, tile_row,
              tile_exp, ntiles, out};
   return launch_gemm(a, max_tiles, true, stream);
+}
+
+extern "C" int qmoe_gather_qmm_swiglu_sorted_tiles(const uint16_t* x, const int32_t* x_rows, int64_t n_rows,
+                                                   int64_t K, const uint32_t* wp, const uint32_t* sb,
+                                                   int32_t num_experts, int64_t N, const int32_t* offsets,
+                                                   const int32_t* tile_row, const int32_t* tile_exp,
+                                                   const int32_t* ntiles, int64_t max_tiles, uint16_t* h,
+                                                   void* stream) {
+  const int rc = check_common(x, n_rows, K, num_experts, N, offsets, tile_row, tile_exp, ntiles, max_tiles, h);
+  if (rc != QMOE_OK || n_rows == 0 || max_tiles == 0) return rc;
+  if (!wp || !sb) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (K % 64) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 64", (long long)K);
+  if (!qmoe::aligned16(wp) || !qmoe::aligned16(sb))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "wp and sb must be 16-byte aligned");
+  GemmArgs a{x, x_rows, n_rows, (int)K, wp, nullptr, nullptr, sb, num_experts, (int)N, offsets, tile_row,
+             tile_exp, ntiles, h};
+  return launch_gemm(a, max_tiles, true, stream, true);
 }
 
 namespace qmoe_gemm {

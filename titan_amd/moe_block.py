@@ -1,0 +1,128 @@
+"""The routed mixture-of-experts block as one call
+(titan/adapters/mlx/vendor/mlx_vlm/models/qwen3_5_moe/language.py:45-91,
+Qwen3_5MoeSparseMoeBlock.__call__, with the fused router of
+engine/patches/decode-fusion/fused_kernels.py:232-371).
+
+    logits  = x @ W_router^T                         fp32 (library GEMM)
+    idx, sc = top-k of logits, softmax over the k    qmoe_router_topk
+    decode  (T * k < 64, switch_layers.py:218):
+        h   = silu(x W_gate^T) * (x W_up^T)          qmoe_moe_gate_up_swiglu
+        y   = sum_j sc_j * W_down[idx_j] h_j          qmoe_moe_down_wsum
+    prefill:
+        order, tiles = stable sort of the pairs       qmoe_route
+        h   = SwiGLU gate_up grouped GEMM             qmoe_gather_qmm_swiglu_sorted_tiles
+        yd  = down grouped GEMM over h                qmoe_gather_qmm_sorted_tiles
+        y   = un-permute + weighted sum               qmoe_weighted_sum
+
+Expert selection follows the fused router, not stock MLX: top-k on fp32
+logits with ties to the lower expert index, scores in fp32.  Stock rounds the
+softmax to bf16 first and breaks bf16 ties arbitrarily
+(decode-fusion/REPORT.md:65-78), so the two can pick different experts on
+near-ties; everything after the selection has the same semantics.
+
+The optional shared expert (language.py:81-89: a dense SwiGLU MLP gated by
+sigmoid(x w_gate)) runs through the same kernels as a one-expert table.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+
+__all__ = ["SparseMoeBlock", "SharedExpert", "DECODE_MAX_PAIRS"]
+
+# switch_layers.py:218: SwitchGLU sorts when indices.size >= 64
+DECODE_MAX_PAIRS = 64
+
+
+@dataclass
+class SharedExpert:
+    """Dense quantized SwiGLU MLP and its scalar gate (language.py:51-53, 81-89):
+    gate_up (w, s, b) [1, 2S, H*bits/32] gate rows first, down (w, s, b)
+    [1, H, S*bits/32], gate weight bf16 [1, H]."""
+
+    gate_up: tuple
+    down: tuple
+    gate_weight: torch.Tensor
+
+
+class SparseMoeBlock:
+    """Routed experts of one MoE layer over MLX-affine 4-bit weights.
+
+    ``router_weight`` bf16 [E, H]; ``gate_up`` = (w, scales, biases) of the
+    fused [E, 2I, H] projection (gate rows first, loader.py:19-27); ``down`` =
+    (w, scales, biases) of [E, H, I].  The prefill copies of both weights are
+    repacked into the tile layout once, here (the gate_up copy in the
+    gate/up-paired row order of the SwiGLU GEMM)."""
+
+    def __init__(self, router_weight: torch.Tensor, gate_up: tuple, down: tuple, top_k: int,
+                 norm_topk_prob: bool = True, wsum_mode: str = "fast", group_size: int = ops.GROUP,
+                 bits: int = ops.BITS, shared: SharedExpert | None = None, prefill_tiles: bool = True):
+        self.router_weight = router_weight
+        self.gate_up = tuple(gate_up)
+        self.down = tuple(down)
+        self.top_k = int(top_k)
+        self.norm = bool(norm_topk_prob)
+        self.wsum_mode = wsum_mode
+        self.group_size, self.bits = group_size, bits
+        self.num_experts = int(gate_up[0].shape[0])
+        self.hidden = int(down[0].shape[1])
+        self.intermediate = int(gate_up[0].shape[1]) // 2
+        self.gu_tiles = self.down_tiles = None
+        if prefill_tiles:
+            self.gu_tiles = ops.repack_tiles(*self.gate_up, group_size, bits, swiglu_pairs=True)
+            self.down_tiles = ops.repack_tiles(*self.down, group_size, bits)
+        self.shared = shared
+        self._shared_tiles = None
+        if shared is not None and prefill_tiles:
+            self._shared_tiles = (ops.repack_tiles(*shared.gate_up, group_size, bits, swiglu_pairs=True),
+                                  ops.repack_tiles(*shared.down, group_size, bits))
+
+    # ------------------------------------------------------------- router
+    def route(self, x2: torch.Tensor):
+        """(idx int32 [T, k], scores fp32 [T, k]) for tokens x2 [T, H]."""
+        logits = torch.matmul(x2.float(), self.router_weight.float().t())
+        return ops.router_topk(logits, self.top_k, self.norm)
+
+    # ------------------------------------------------------------- experts
+    def experts(self, x2: torch.Tensor, idx: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
+        """sum_j scores[t, j] * expert_{idx[t, j]}(x2[t]) for x2 [T, H]."""
+        T = x2.shape[0]
+        k = idx.shape[-1]
+        if T * k < DECODE_MAX_PAIRS or self.gu_tiles is None:
+            h = ops.gate_up_silu(x2, *self.gate_up, idx, self.group_size, self.bits)
+            return ops.down_wsum(h, *self.down, idx, scores, self.group_size, self.bits)
+        r = ops.route(idx, self.num_experts)
+        lhs = torch.div(r.order, k, rounding_mode="floor").to(torch.int32)
+        h = ops.gather_qmm_swiglu_sorted_tiles(x2, self.gu_tiles, r.tiles, x_rows=lhs)
+        yd = ops.gather_qmm_sorted_tiles(h, self.down_tiles, r.tiles)
+        return ops.moe_weighted_sum(yd, r.inv_order, scores, (T, self.hidden), self.wsum_mode)
+
+    def shared_expert(self, x2: torch.Tensor) -> torch.Tensor:
+        """sigmoid(x w_gate) * SwiGLU-MLP(x) (language.py:81-89)."""
+        sh = self.shared
+        T = x2.shape[0]
+        zeros = torch.zeros(T, 1, dtype=torch.int32, device=x2.device)
+        ones = torch.ones(T, 1, dtype=torch.float32, device=x2.device)
+        if T <= 16 or self._shared_tiles is None:  # the fused down kernel takes up to 16 tokens
+            h = ops.gate_up_silu(x2, *sh.gate_up, zeros, self.group_size, self.bits)
+            y = ops.down_wsum(h, *sh.down, zeros, ones, self.group_size, self.bits)
+        else:
+            gu_t, dn_t = self._shared_tiles
+            tiles = ops.build_tiles(zeros.reshape(-1), 1)
+            h = ops.gather_qmm_swiglu_sorted_tiles(x2, gu_t, tiles)
+            y = ops.gather_qmm_sorted_tiles(h, dn_t, tiles)
+        g = torch.sigmoid(torch.matmul(x2.float(), sh.gate_weight.float().t()))
+        return (g * y.float()).to(torch.bfloat16)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        H = x.shape[-1]
+        x2 = x.reshape(-1, H).to(torch.bfloat16).contiguous()
+        idx, scores = self.route(x2)
+        y = self.experts(x2, idx, scores)
+        if self.shared is not None:
+            y = (y.float() + self.shared_expert(x2).float()).to(torch.bfloat16)
+        return y.reshape(x.shape)

@@ -271,27 +271,45 @@ class TileWeights:
     K: int
     group_size: int = GROUP
     bits: int = BITS
+    swiglu_pairs: bool = False  # rows in the gate/up-paired order of qmoe_gather_qmm_swiglu_sorted_tiles
 
     @property
     def nbytes(self) -> int:
         return self.wp.numel() * 4 + self.sb.numel() * 4
 
 
+def swiglu_pair_order(N: int, device=None) -> torch.Tensor:
+    """Row order of a fused [gate(I) | up(I)] weight in which every 64-row
+    block holds 32 gate rows and the up rows of the same 32 indices: row
+    64c + j is gate row 32c + j (j < 32) or up row I + 32c + j - 32."""
+    if N % 64:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"N={N}: gate/up pairing needs N % 64 == 0")
+    I = N // 2
+    t = torch.arange(N, device=device)
+    c, j = t // 64, t % 64
+    return torch.where(j < 32, 32 * c + j, I + 32 * c + j - 32)
+
+
 def repack_tiles(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = GROUP,
-                 bits: int = BITS) -> TileWeights:
-    """MLX-layout expert weights [E, N, K/8] -> :class:`TileWeights`."""
+                 bits: int = BITS, swiglu_pairs: bool = False) -> TileWeights:
+    """MLX-layout expert weights [E, N, K/8] -> :class:`TileWeights`.  With
+    ``swiglu_pairs`` a fused gate_up weight is first put in the gate/up-paired
+    row order (:func:`swiglu_pair_order`) for the SwiGLU-epilogue GEMM."""
     w, scales, biases = _words(w, "w"), _bf16(scales, "scales"), _bf16(biases, "biases")
     if w.dim() != 3:
         raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"w must be [E, N, K/8], got {tuple(w.shape)}")
     E, N, KW = w.shape
     K = KW * 32 // bits
     _check_quant(w, scales, group_size, bits, K)
+    if swiglu_pairs:
+        perm = swiglu_pair_order(N, w.device)
+        w, scales, biases = (t.index_select(1, perm).contiguous() for t in (w, scales, biases))
     G = K // group_size
     wp = torch.empty(E, max(N // 64, 0), G, 2, 2, 32, 4, dtype=torch.int32, device=w.device)
     sb = torch.empty(E, max(N // 64, 0), G, 64, dtype=torch.int32, device=w.device)
     _lib.call("qmoe_repack_tiles", w.data_ptr(), scales.data_ptr(), biases.data_ptr(), E, N, K, group_size, bits,
               wp.data_ptr(), sb.data_ptr(), _stream(w))
-    return TileWeights(wp, sb, E, N, K, group_size, bits)
+    return TileWeights(wp, sb, E, N, K, group_size, bits, swiglu_pairs)
 
 
 def gather_qmm_sorted_tiles(x: torch.Tensor, tw: TileWeights, tiles: TileTable,
@@ -551,9 +569,47 @@ def gather_qmm_int8_sorted_tiles(xi: torch.Tensor, sx: torch.Tensor, tw: TileWei
     return out
 
 
+def gather_qmm_swiglu_sorted_tiles(x: torch.Tensor, tw: TileWeights, tiles: TileTable,
+                                   x_rows: torch.Tensor | None = None) -> torch.Tensor:
+    """gate_up grouped GEMM with SwiGLU fused: h [rows, N/2] = silu(gate) * up
+    over gate/up-paired tile weights (``repack_tiles(..., swiglu_pairs=True)``)."""
+    if not tw.swiglu_pairs:
+        raise ValueError("the SwiGLU GEMM needs weights repacked with swiglu_pairs=True")
+    x = _bf16(x, "x")
+    K = x.shape[-1]
+    if K != tw.K:
+        raise ValueError(f"x has K={K}, the weights K={tw.K}")
+    if tiles.num_experts != tw.num_experts or tiles.tile_rows != tile_rows():
+        raise ValueError("tile table does not match this call")
+    x2 = x.reshape(-1, K)
+    xr = None if x_rows is None else _i32(x_rows.reshape(-1), "x_rows", x.device)
+    h = torch.empty(tiles.rows, tw.N // 2, dtype=torch.bfloat16, device=x.device)
+    _lib.call("qmoe_gather_qmm_swiglu_sorted_tiles", x2.data_ptr(), _ptr(xr), tiles.rows, K, tw.wp.data_ptr(),
+              tw.sb.data_ptr(), tw.num_experts, tw.N, tiles.offsets.data_ptr(), tiles.tile_row.data_ptr(),
+              tiles.tile_exp.data_ptr(), tiles.ntiles.data_ptr(), tiles.maxt, h.data_ptr(), _stream(x))
+    return h
+
+
+def router_topk(logits: torch.Tensor, k: int, norm: bool = True):
+    """Top-k experts per token from router logits, (idx int32 [T, k], scores
+    float32 [T, k]); descending, ties to the lower expert index.  norm: the
+    softmax renormalised over the chosen experts, else the full softmax
+    (qwen3_5_moe/language.py:65-71, decode-fusion/fused_kernels.py:363-371)."""
+    _dev(logits, "logits")
+    lg = _ready(logits.float())
+    E = lg.shape[-1]
+    lg2 = lg.reshape(-1, E)
+    T = lg2.shape[0]
+    idx = torch.empty(T, k, dtype=torch.int32, device=lg.device)
+    scores = torch.empty(T, k, dtype=torch.float32, device=lg.device)
+    _lib.call("qmoe_router_topk", lg2.data_ptr(), T, E, k, int(bool(norm)), idx.data_ptr(), scores.data_ptr(),
+              _stream(lg))
+    return idx.reshape(*lg.shape[:-1], k), scores.reshape(*lg.shape[:-1], k)
+
+
 __all__ = [
     "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "TileWeights", "Routing", "build_tiles", "route",
-    "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmm_int8_sorted_tiles", "gather_qmv_tiles", "gate_up_silu_tiles",
+    "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmm_int8_sorted_tiles", "router_topk", "gather_qmm_swiglu_sorted_tiles", "swiglu_pair_order", "gather_qmv_tiles", "gate_up_silu_tiles",
     "max_tiles", "tile_rows", "unpack", "dequantize", "gather_qmv", "gather_qmm_sorted", "gather_qmm",
     "gemm_supported", "quantized_matmul", "gate_up_silu", "down_wsum", "moe_weighted_sum",
     "quantize_act_int8", "gather_qmm_int8_sorted",
