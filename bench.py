@@ -438,7 +438,7 @@ def setup_cfg3(args, dev):
 
     return wl, [mk_tiles(i) for i in range(steps)], {
         "flops": synth.algorithmic_flops(3, wl), "bound": "mfma", "peak_tflops": BF16_PEAK_TFLOPS,
-        "kernel": "gemm_bf16_kernel<true>", "sets": len(sets),
+        "kernel": "gemm_bf16_kernel<true, false>", "sets": len(sets),
         "alt": ("mlx_layout_us_per_call", [mk_mlx(i) for i in range(steps)]),
         "workload": "prefill grouped GEMM: 4096 tokens x top-10 Zipf(1.1) routed rows sorted by expert, "
                     "gate_up W [256,1024,2048] int4 g64 (tile layout, repacked at load), x gathered "

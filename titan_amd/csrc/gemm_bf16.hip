@@ -3,14 +3,16 @@
 // Semantics: titan/kernels/moe_gather_ws.py:20-32 -- weights dequantised to
 // bf16 as bf16_rne(fmaf(q, s, b)) (:343-344), bf16 x bf16 products, fp32
 // accumulation.  Work unit: one (tile, column block).  A tile is up to
-// kBM = 256 consecutive sorted rows of one expert (the tile list of the
+// kBM = 128 consecutive sorted rows of one expert (the tile list of the
 // routing step); a column block is kBN = 256 output columns, one 64-column
 // slice for each of the block's four waves.  Every wave covers all the
 // tile's rows, so each weight element is dequantised once per tile.
+// Persistent blocks, two per CU, take the units heavy-first in a snake over
+// XCD-contiguous slots (gemm_common.h).
 //
-// Register budget: one wave per SIMD, so a wave may hold 512 registers.  Its
-// 256 x 64 output tile is 8 x 2 subtiles of 32 x 32 fp32 (256 accumulator
-// registers, in AGPRs); operands and addresses use the VGPRs.
+// Register budget: two waves per SIMD (two blocks per CU), so a wave may hold
+// 256 registers.  Its 128 x 64 output tile is 4 x 2 subtiles of 32 x 32 fp32
+// (128 accumulator registers); operands and addresses use the rest.
 //
 // Per 64-wide K group (one quantisation group) a wave
 //   - dequantises its 64 columns' codes in registers (two 16-byte code
@@ -20,7 +22,7 @@
 //     v_fma_mix_f32 widens them exactly and computes
 //     fma(q * 2^-24, s * 2^24, b) == fmaf(q, s, b) bit for bit (scaling by a
 //     power of two is exact), then v_cvt_pk_bf16_f32 rounds to nearest even;
-//   - runs 4 k-steps x 16 v_mfma_f32_32x32x16_bf16, weights as the A operand
+//   - runs 4 k-steps x 2 * MSUB (<= 8) v_mfma_f32_32x32x16_bf16, weights as the A operand
 //     (rows = output columns) and activations as B (columns = token rows), so
 //     each lane ends up owning four consecutive output columns per register
 //     quad and the epilogue stores 8 bytes at a time.
@@ -30,12 +32,12 @@
 // in flight across iterations with explicit wait counts) into a ring of
 // kStages stages.  A stage holds
 //   A  the tile's activation rows for the group, gathered through x_rows,
-//      256 x 128 bytes, 16-byte units XOR-swizzled by row (swz) so operand
+//      128 x 128 bytes, 16-byte units XOR-swizzled by row (swz) so operand
 //      reads are bank-conflict free; only the subtiles the tile has are copied;
 //   B  each wave's 64 columns of packed codes (16 bytes per lane and subtile);
 //   S  the 64 columns' scales and biases.
 // Row subtiles past a tile's valid rows are compiled out (the loop is
-// instantiated per subtile count 1..8), so a short tile costs only its own
+// instantiated per subtile count 1..4), so a short tile costs only its own
 // MFMAs and copies.
 //
 // K order inside a group is free as long as A and B agree: lane half h

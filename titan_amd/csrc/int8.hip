@@ -67,18 +67,17 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restri
 //      chunk; MLX layout: 16 bytes per lane from the column's row);
 //   S  the columns' scales and biases.
 // A wave turns its code words into int8 with byte permutes (codes 0..15 are
-// valid int8: no zero point), runs v_mfma_i32_32x32x32_i8 twice per 32 x 32
-// subtile (D_g exact in int32) and folds acc += s * D_g in fp32; the wave
-// whose index matches a row subtile also takes that subtile's exact row sums
-// R_g with v_dot4 and keeps them in LDS as int16 (|R_g| <= 64 * 127).  After
-// the last group the bias term sum_g b[n,g] R_g[m] is one small bf16 MFMA
+// valid int8: no zero point), runs one v_mfma_i32_16x16x64_i8 per 16 x 16
+// subtile and group (D_g exact in int32) and folds acc += s * D_g in fp32;
+// wave w < the tile's 16-row subtile count also takes subtile w's exact row
+// sums R_g with v_dot4 and keeps them in LDS as int16 (|R_g| <= 64 * 127).
+// After the last group the bias term sum_g b[n,g] R_g[m] is a small bf16 MFMA
 // product per subtile (R split into exact bf16 hi + lo), the rows are scaled
 // by sx and the tile leaves through LDS as 512-byte row segments.
 //
-// K order inside a group is free as long as both operands agree: MFMA k-half
-// kk of a group takes, for lane half h, group elements 32h + 16kk .. +15 --
-// code words 2kk, 2kk+1 of the lane's 16-byte code chunk and 16-byte unit
-// 2h + kk of the activation row.
+// K order inside a group is free as long as both operands agree: lane
+// quarter qq of the 16 x 16 x 64 MFMA supplies group elements 16qq .. +15 of
+// its row and of its column (tile_loop_i8).
 
 using namespace qmoe_gemm;
 
