@@ -41,7 +41,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="0,1,2,3,4")
+    ap.add_argument("--configs", default="0,1,2,3,4,5,6,7",
+                    help="0-4 the five workloads, 5 workload 0 with 8-bit codes, 6 the decode-width sweep, "
+                         "7 the whole MoE block")
     ap.add_argument("--rotate-gb", type=float, default=1.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -492,7 +494,155 @@ def setup_cfg4(args, dev):
                     "-> [40960,1024]"}
 
 
-SETUPS = {0: setup_cfg0, 1: setup_cfg1, 2: setup_cfg2, 3: setup_cfg3, 4: setup_cfg4}
+def setup_cfg5(args, dev):
+    """Workload 0 with 8-bit codes (the small-M kernel's other bit width)."""
+    import torch
+    from titan_amd import ops, synth
+
+    wl = synth.make(5)
+    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 105)
+    x = to_dev(wl["x"], "bf16", dev)
+    out = torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+
+    def mk(i):
+        w, s, b = sets[i % len(sets)]
+
+        def f():
+            ops._lib.call("qmoe_quantized_matmul", x.data_ptr(), 1, 2048, w.data_ptr(), s.data_ptr(),
+                          b.data_ptr(), 4096, 64, 8, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        return f
+
+    return wl, [mk(i) for i in range(args.steps)], {
+        "bytes": synth.algorithmic_bytes(5), "flops": synth.algorithmic_flops(5), "bound": "hbm",
+        "kernel": "qmv_kernel<4, 16, 0, 8>", "sets": len(sets),
+        "workload": "dense quantized_matmul x [1,2048] . W [4096,2048] int8 codes g64"}
+
+
+WIDTHS = (1, 2, 4, 6, 8, 16)
+
+
+def run_widths(args, dev):
+    """Decode widths: T tokens x top-10 of 256 experts through the gate_up +
+    SwiGLU step two ways -- the decode GEMV (qmoe_moe_gate_up_swiglu) and the
+    sorted path (qmoe_route + the SwiGLU-epilogue grouped GEMM) -- on the
+    workload-1 weights.  GB/s counts each distinct expert's bytes once."""
+    import torch
+    from titan_amd import ops, synth
+
+    wl = synth.make(1)
+    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 106)
+    tsets = [ops.repack_tiles(w, s, b, swiglu_pairs=True) for (w, s, b) in sets]
+    rng = np.random.default_rng(1006)
+    per_expert = 2 * 512 * (2048 // 2 + 32 * 4)
+    res = {}
+    for T in WIDTHS:
+        x = to_dev(synth.bf16_bits(rng.normal(size=(T, 2048)).astype(np.float32)), "bf16", dev)
+        idx_np = [np.stack([rng.choice(256, 10, replace=False) for _ in range(T)]).astype(np.int32)
+                  for _ in sets]
+        idx = [torch.from_numpy(a).to(dev) for a in idx_np]
+        distinct = float(np.mean([np.unique(a).size for a in idx_np]))
+        h = torch.empty(T * 10, 512, dtype=torch.bfloat16, device=dev)
+        routes = [ops.route(i, 256) for i in idx]
+        lhs = [torch.div(r.order, 10, rounding_mode="floor").to(torch.int32) for r in routes]
+        torch.cuda.synchronize()
+
+        def mk_dec(i, T=T, x=x, idx=idx, h=h):
+            w, s, b = sets[i % len(sets)]
+            ix = idx[i % len(sets)]
+
+            def f():
+                ops._lib.call("qmoe_moe_gate_up_swiglu", x.data_ptr(), ix.data_ptr(), T, 10, 2048, w.data_ptr(),
+                              s.data_ptr(), b.data_ptr(), 256, 512, 64, 4, h.data_ptr(),
+                              torch.cuda.current_stream().cuda_stream)
+            return f
+
+        def mk_sorted(i, T=T, x=x, h=h):
+            j = i % len(sets)
+            tw, r, lh = tsets[j], routes[j], lhs[j]
+            t = r.tiles
+            ws = torch.empty(max(int(ops._lib.load().qmoe_route_workspace_size(T * 10, 256)), 256) // 4,
+                             dtype=torch.int32, device=dev)
+            flat = idx[j].reshape(-1)
+
+            def f():
+                st = torch.cuda.current_stream().cuda_stream
+                ops._lib.call("qmoe_route", flat.data_ptr(), T * 10, 256, t.tile_rows, r.order.data_ptr(),
+                              r.inv_order.data_ptr(), r.sorted_ids.data_ptr(), t.offsets.data_ptr(),
+                              t.tile_row.data_ptr(), t.tile_exp.data_ptr(), t.ntiles.data_ptr(), t.maxt,
+                              ws.data_ptr(), ws.numel() * 4, st)
+                ops._lib.call("qmoe_gather_qmm_swiglu_sorted_tiles", x.data_ptr(), lh.data_ptr(), T * 10, 2048,
+                              tw.wp.data_ptr(), tw.sb.data_ptr(), 256, 1024, t.offsets.data_ptr(),
+                              t.tile_row.data_ptr(), t.tile_exp.data_ptr(), t.ntiles.data_ptr(), t.maxt,
+                              h.data_ptr(), st)
+            return f
+
+        steps = max(8, args.steps // 2)
+        sec_d, _ = (time_eager if args.eager else time_graph)([mk_dec(i) for i in range(steps)], args.warmup, dev)
+        sec_s, _ = (time_eager if args.eager else time_graph)([mk_sorted(i) for i in range(steps)], args.warmup,
+                                                              dev)
+        nbytes = distinct * per_expert + T * 2048 * 2 + T * 10 * 512 * 2
+        res[T] = {"pairs": T * 10, "distinct_experts": distinct, "decode_us": round(sec_d * 1e6, 3),
+                  "decode_GBps": round(nbytes / sec_d / 1e9, 1), "sorted_us": round(sec_s * 1e6, 3),
+                  "sorted_GBps": round(nbytes / sec_s / 1e9, 1),
+                  "faster": "decode" if sec_d <= sec_s else "sorted"}
+        print(f"[bench] width T={T}: {res[T]}", file=sys.stderr, flush=True)
+        del routes, lhs, idx
+    return {"workload": "decode widths: T tokens x top-10 of E=256, gate_up + SwiGLU, W [256,1024,2048] int4 g64; "
+                        "decode GEMV vs route + SwiGLU grouped GEMM",
+            "kernel": "qmv64_kernel<1, 1, 4, 64, true, false> | route_* + gemm_bf16_kernel<true, true>",
+            "widths": res}
+
+
+def run_block(args, dev):
+    """The whole routed MoE block (titan_amd.moe_block.SparseMoeBlock) as one
+    call: router logits, top-k, then the decode kernels (T = 1) or routing
+    sort + SwiGLU GEMM + down GEMM + weighted sum (T = 4096), E = 256,
+    H = 2048, I = 512, top-10, random weights rotated over several blocks."""
+    import torch
+    from titan_amd import moe_block, synth
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(107)
+
+    def block():
+        gu = (random_like_words((256, 1024, 256), dev, gen), random_scales((256, 1024, 32), dev, gen),
+              random_biases((256, 1024, 32), dev, gen))
+        dn = (random_like_words((256, 2048, 64), dev, gen), random_scales((256, 2048, 8), dev, gen),
+              random_biases((256, 2048, 8), dev, gen))
+        router = (torch.randn(256, 2048, device=dev, generator=gen) * 0.05).to(torch.bfloat16)
+        return moe_block.SparseMoeBlock(router, gu, dn, 10)
+
+    rng = np.random.default_rng(1007)
+    res = {}
+    per_gu, per_dn = 1024 * (1024 + 32 * 4), 2048 * (256 + 8 * 4)
+    for T, nblocks in ((1, 4), (4096, 2)):
+        blocks = [block() for _ in range(nblocks)]
+        x = to_dev(synth.bf16_bits(rng.normal(size=(T, 2048)).astype(np.float32)), "bf16", dev)
+        torch.cuda.synchronize()
+        steps = args.steps if T == 1 else max(1, args.steps // 10)
+        fns = [(lambda b=blocks[i % nblocks]: b(x)) for i in range(steps)]
+        sec, tinfo = (time_eager if args.eager else time_graph)(fns, args.warmup if T == 1 else 2, dev)
+        r = {"us_per_call": round(sec * 1e6, 3), "us_per_call_min": round(tinfo["min"] * 1e6, 3)}
+        if T == 1:
+            nbytes = 256 * 2048 * 2 + 10 * (per_gu + per_dn) + 2048 * 2 * 2
+            r.update(metric="HBM GB/s", value=round(nbytes / sec / 1e9, 1), bytes_per_call=nbytes,
+                     pct_hbm_peak=round(100 * nbytes / sec / 1e9 / HBM_PEAK_GBS, 2),
+                     path="router + top-k + gate_up/SwiGLU GEMV + down/weighted-sum GEMV")
+        else:
+            fl = 2 * T * 10 * 2048 * 1024 + 2 * T * 10 * 512 * 2048 + 2 * T * 2048 * 256
+            r.update(metric="TFLOP/s", value=round(fl / sec / 1e12, 1), flops_per_call=fl,
+                     pct_bf16_peak=round(100 * fl / sec / 1e12 / BF16_PEAK_TFLOPS, 2),
+                     path="router + top-k + route + SwiGLU GEMM + down GEMM + weighted sum")
+        res[T] = r
+        print(f"[bench] block T={T}: {r}", file=sys.stderr, flush=True)
+        del blocks, fns, tinfo
+        torch.cuda.empty_cache()
+    return {"workload": "whole MoE block, E=256, H=2048, I=512, top-10, int4 g64 (tile layout for prefill)",
+            "tokens": res}
+
+
+SETUPS = {0: setup_cfg0, 1: setup_cfg1, 2: setup_cfg2, 3: setup_cfg3, 4: setup_cfg4, 5: setup_cfg5}
 
 
 # ------------------------------------------------------------- CPU baseline
@@ -572,6 +722,10 @@ def main():
     head = None
     for cfg in cfgs:
         print(f"[bench] workload {cfg}: setup", file=sys.stderr, flush=True)
+        if cfg in (6, 7):
+            results[cfg] = (run_widths if cfg == 6 else run_block)(args, dev)
+            torch.cuda.empty_cache()
+            continue
         wl, fns, meta = SETUPS[cfg](args, dev)
         print(f"[bench] workload {cfg}: timing {len(fns)} steps", file=sys.stderr, flush=True)
         sec, tinfo = (time_eager if args.eager else time_graph)(fns, args.warmup, dev)

@@ -103,7 +103,9 @@ int qmoe_build_tiles(const int32_t* sorted_ids, int64_t n_rows,
  * Matrix-vector kernel: every row streams its expert's weights, so this is the
  * decode / small-batch path.  fp32 accumulation of the factored affine form
  * s*sum(x*q) + b*sum(x) (engine/patches/decode-fusion/fused_kernels.py:57-79),
- * bf16 output. */
+ * bf16 output.  bits 4 or 8 (8-bit codes need K = 32*L*n with L in {4, 8, 16}
+ * and n <= 8, so K <= 4096), group_size 32, 64 or 128
+ * (engine/patches/smallm/kernel.py:38, 319-327). */
 int qmoe_gather_qmv(const uint16_t* x, const int32_t* x_rows,
                     const int32_t* experts, int64_t n_rows, int64_t K,
                     const uint32_t* w, const uint16_t* scales,
@@ -112,7 +114,8 @@ int qmoe_gather_qmv(const uint16_t* x, const int32_t* x_rows,
 
 /* mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)
  * for x [M, K] (titan/adapters/mlx/compiled.py:209-218; small-M drop-in
- * engine/patches/smallm/kernel.py:333-391): out [M, N]. */
+ * engine/patches/smallm/kernel.py:333-391): out [M, N].  Same bit widths and
+ * group sizes as qmoe_gather_qmv. */
 int qmoe_quantized_matmul(const uint16_t* x, int64_t M, int64_t K,
                           const uint32_t* w, const uint16_t* scales,
                           const uint16_t* biases, int64_t N, int group_size,
@@ -285,6 +288,26 @@ int qmoe_gather_qmm_swiglu_sorted_tiles(const uint16_t* x, const int32_t* x_rows
  * softmax probability.  k <= 64, E <= 1024; logits are expected finite. */
 int qmoe_router_topk(const float* logits, int64_t T, int64_t E, int64_t k,
                      int norm, int32_t* idx, float* scores, void* stream);
+
+/* Router logits in fp32 from an affine-quantized router weight [E, K*bits/32]
+ * (replaces the fused router's quantized matvec,
+ * engine/patches/decode-fusion/fused_kernels.py:232-260, 353-363):
+ * logits[t, e] = s*sum(x*q) + b*sum(x) per group, fp32 accumulation, no
+ * dequantised weight.  The GEMV kernels of qmoe_quantized_matmul with an fp32
+ * store; same bit widths and group sizes. */
+int qmoe_router_logits(const uint16_t* x, int64_t T, int64_t K,
+                       const uint32_t* w, const uint16_t* scales,
+                       const uint16_t* biases, int64_t E, int group_size,
+                       int bits, float* logits, void* stream);
+
+/* Router logits in fp32 from a dense bf16 router weight [E, K] (the
+ * unquantised nn.Linear gate, qwen3_5_moe/language.py:52, 61):
+ * logits[t, e] = sum_k x[t, k] * W[e, k], fp32 accumulation.  K % 8 == 0.
+ * One wave per (token, expert): meant for decode widths; a prefill caller
+ * uses a GEMM library. */
+int qmoe_router_logits_dense(const uint16_t* x, int64_t T, int64_t K,
+                             const uint16_t* w, int64_t E, float* logits,
+                             void* stream);
 
 #ifdef __cplusplus
 }

@@ -25,7 +25,7 @@ def ckpt(tmp_path_factory):
     return d, layers, config
 
 
-def _direct(a, dev, router_bits_ref, k):
+def _direct(a, dev, k):
     def trio(t):
         return words_t(t[0], dev), bf16_t(t[1], dev), bf16_t(t[2], dev)
 
@@ -34,7 +34,10 @@ def _direct(a, dev, router_bits_ref, k):
     if "sg" in a:
         sgu = tuple(np.concatenate([g, u], axis=1) for g, u in zip(a["sg"], a["su"]))
         shared = moe_block.SharedExpert(trio(sgu), trio(a["sd"]), bf16_t(a["sgate"], dev))
-    return moe_block.SparseMoeBlock(bf16_t(router_bits_ref, dev), trio(gu), trio(a["down"]), k, shared=shared)
+    if "router_q" in a:
+        return moe_block.SparseMoeBlock(trio(a["router_q"]), trio(gu), trio(a["down"]), k, shared=shared,
+                                        router_quant=(64, 8))
+    return moe_block.SparseMoeBlock(bf16_t(a["router"], dev), trio(gu), trio(a["down"]), k, shared=shared)
 
 
 @pytest.mark.parametrize("layer", [0, 1])
@@ -48,13 +51,17 @@ def test_loaded_block_matches_direct_block(dev, orc, ckpt, layer, T):
     k = config["text_config"]["num_experts_per_tok"]
     assert blk.top_k == k and blk.num_experts == a["gate"][0].shape[0]
     if "router_q" in a:
+        # kept quantised; the prefill GEMM's copy is the bf16 dequantisation
         w, s, b = a["router_q"]
+        assert blk.router_quant == (64, 8)
+        assert np.array_equal(blk.router_weight[0].cpu().numpy().view(np.uint32), w)
         want_router = orc.dequantize_bf16(w, s, b, 64, 8)
     else:
+        assert np.array_equal(bits(blk.router_weight), a["router"])
         want_router = a["router"]
-    assert np.array_equal(bits(blk.router_weight), want_router)
+    assert np.array_equal(blk._router_f32.cpu().numpy(), orc.f32_from_bf16(want_router))
     assert (blk.shared is not None) == ("sg" in a)
-    ref = _direct(a, dev, want_router, k)
+    ref = _direct(a, dev, k)
     rng = np.random.default_rng(T + layer)
     x = bf16_t(synth.bf16_bits(rng.normal(size=(T, a["gate"][0].shape[2] * 8)).astype(np.float32)), dev)
     y, yr = blk(x), ref(x)

@@ -53,6 +53,47 @@ def test_router_topk_ties_take_lower_index(dev, orc):
     np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
 
 
+def _assert_logits(got, ref64, absx_absw):
+    """fp32 accumulation bound: |got - ref| <= 2^-16 * sum_k |x_k||w_k| per
+    element (K * 2^-24 for K <= 256 terms per lane chain, with room); one
+    dropped or doubled term moves a logit by ~1/K of that sum, far above."""
+    err = np.abs(got.astype(np.float64) - ref64)
+    bound = 2.0 ** -16 * absx_absw
+    print(f"[parity] logits max err/bound {np.max(err / bound):.3g}", flush=True)
+    assert np.all(err <= bound)
+
+
+@pytest.mark.parametrize("T,E,K", [(1, 256, 2048), (5, 128, 1024), (16, 512, 4096), (3, 64, 200)])
+def test_router_logits_dense(dev, orc, T, E, K):
+    say(f"router logits dense T={T} E={E} K={K}")
+    rng = np.random.default_rng(T * E + K)
+    x = synth.bf16_bits(rng.normal(size=(T, K)).astype(np.float32))
+    w = synth.bf16_bits((rng.normal(size=(E, K)) * 0.05).astype(np.float32))
+    got = ops.router_logits(bf16_t(x, dev), bf16_t(w, dev)).cpu().numpy()
+    xf, wf = orc.f32_from_bf16(x).astype(np.float64), orc.f32_from_bf16(w).astype(np.float64)
+    _assert_logits(got, xf @ wf.T, np.abs(xf) @ np.abs(wf).T)
+
+
+@pytest.mark.parametrize("nbits,gs", [(4, 64), (8, 64), (8, 32), (4, 128)])
+def test_router_logits_quantized(dev, orc, nbits, gs):
+    say(f"router logits quantized bits={nbits} gs={gs}")
+    T, E, K = 3, 256, 2048
+    rng = np.random.default_rng(nbits * gs)
+    w, s, b = synth.quant_weights(rng, (E,), K, group_size=gs, bits=nbits)
+    x = synth.bf16_bits(rng.normal(size=(T, K)).astype(np.float32))
+    got = ops.router_logits(bf16_t(x, dev), (words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev)), gs, nbits)
+    ref64 = np.stack([orc.gather_qmm_rows(x[t:t + 1], None, np.zeros(1, np.int32), w[None], s[None], b[None],
+                                          group_size=gs, bits=nbits)[0][0] for t in range(T)])
+    # the kernel sums x * (128 + q) per chunk before the affine correction
+    # (qmoe_router_logits), so its rounding scales with those magnitudes:
+    # sum_g s_g * (128 + 2^bits) * sum_{k in g} |x_k| + |b_g| * sum_{k in g} |x_k|
+    xg = np.abs(orc.f32_from_bf16(x).astype(np.float64)).reshape(T, K // gs, gs).sum(-1)
+    sf = np.abs(orc.f32_from_bf16(s).astype(np.float64))
+    bf = np.abs(orc.f32_from_bf16(b).astype(np.float64))
+    mag = xg @ (sf * (128 + 2 ** nbits) + bf).T
+    _assert_logits(got.cpu().numpy(), ref64, mag)
+
+
 @pytest.mark.parametrize("E,I,K,counts", [
     (4, 512, 2048, [1, 129, 300, 64]),
     (8, 128, 1024, [7, 0, 33, 97, 128, 200, 2, 65]),
@@ -91,24 +132,26 @@ def _dev_w(t, dev):
     return words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev)
 
 
-@pytest.mark.parametrize("T", [1, 3, 6, 7, 300])
-def test_moe_block_matches_oracle_chain(dev, orc, T):
+@pytest.mark.parametrize("T,smp", [(1, 64), (3, 64), (6, 64), (7, 64), (300, 64), (7, 1000), (16, 1000)])
+def test_moe_block_matches_oracle_chain(dev, orc, T, smp):
     E, H, I, k = 64, 2048, 512, 10
-    say(f"MoE block T={T} E={E} H={H} I={I} k={k}")
+    say(f"MoE block T={T} E={E} H={H} I={I} k={k} sort_min_pairs={smp}")
     gu, dn, router, _ = _block_problem(T + 5, E, H, I)
     rng = np.random.default_rng(T)
     x = synth.bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
-    blk = moe_block.SparseMoeBlock(bf16_t(router, dev), _dev_w(gu, dev), _dev_w(dn, dev), k)
+    blk = moe_block.SparseMoeBlock(bf16_t(router, dev), _dev_w(gu, dev), _dev_w(dn, dev), k, sort_min_pairs=smp)
     xt = bf16_t(x, dev)
     y = bits(blk(xt))
-    # stage 1: the selection, on the block's own fp32 logits
-    logits = torch.matmul(xt.float(), bf16_t(router, dev).float().t()).cpu().numpy()
+    # stage 1: the logits, then the selection on the block's own fp32 logits
+    logits = blk.route_logits(xt).cpu().numpy()
+    xf, wf = orc.f32_from_bf16(x).astype(np.float64), orc.f32_from_bf16(router).astype(np.float64)
+    _assert_logits(logits, xf @ wf.T, np.abs(xf) @ np.abs(wf).T)
     idx, sc = blk.route(xt)
     ridx, rsc = orc.router_topk(logits, k, True)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
     sc32 = sc.cpu().numpy()
-    if T * k < moe_block.DECODE_MAX_PAIRS:
+    if T * k < blk.sort_min_pairs and T <= 16:
         # stage 2: h = silu(gate) * up per (token, slot); stage 3: the fused
         # down + weighted sum, the oracle fed the kernel's own h
         h = ops.gate_up_silu(xt, *blk.gate_up, idx)

@@ -501,3 +501,53 @@ def test_gather_qmv_tiles(dev, orc, R, E, N, K):
     ym = ops.gather_qmv(bf16_t(x, dev), i32_t(xr, dev), i32_t(ex, dev), words_t(w, dev), bf16_t(s, dev),
                         bf16_t(b, dev))
     assert np.array_equal(bits(y), bits(ym))
+
+
+@pytest.mark.parametrize("nbits,gs", [(8, 32), (8, 64), (8, 128), (4, 32), (4, 128)])
+@pytest.mark.parametrize("M,N,K", [(1, 512, 2048), (3, 256, 1024), (16, 128, 4096), (2, 64, 512)])
+def test_quantized_matmul_bits_and_groups(dev, orc, nbits, gs, M, N, K):
+    """The small-M quantized matmul over 4- and 8-bit codes and group sizes
+    32/64/128 (engine/patches/smallm/kernel.py:38, 319-327)."""
+    say(f"quantized_matmul bits={nbits} gs={gs} M={M} N={N} K={K}")
+    rng = np.random.default_rng(nbits * 7919 + gs * 31 + M * N + K)
+    w, s, b = synth.quant_weights(rng, (N,), K, group_size=gs, bits=nbits)
+    x = synth.bf16_bits(rng.normal(size=(M, K)).astype(np.float32))
+    y = ops.quantized_matmul(bf16_t(x, dev), words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), group_size=gs,
+                             bits=nbits)
+    ref64, _ = orc.gather_qmm_rows(x, None, np.zeros(M, np.int32), w[None], s[None], b[None], group_size=gs,
+                                   bits=nbits)
+    assert_close_bf16(orc, bits(y), ref64, what=f"qmm{nbits} gs{gs} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("nbits,gs", [(8, 64), (8, 128), (4, 32)])
+def test_gather_qmv_bits_and_groups(dev, orc, nbits, gs):
+    say(f"gather_qmv bits={nbits} gs={gs}")
+    rng = np.random.default_rng(nbits + gs)
+    E, N, K, R = 6, 192, 2048, 13
+    w, s, b = synth.quant_weights(rng, (E, N), K, group_size=gs, bits=nbits)
+    x = synth.bf16_bits(rng.normal(size=(4, K)).astype(np.float32))
+    xr = rng.integers(0, 4, size=R).astype(np.int32)
+    ex = rng.integers(0, E, size=R).astype(np.int32)
+    y = ops.gather_qmv(bf16_t(x, dev), i32_t(xr, dev), i32_t(ex, dev), words_t(w, dev), bf16_t(s, dev),
+                       bf16_t(b, dev), gs, nbits)
+    ref64, _ = orc.gather_qmm_rows(x, xr, ex, w, s, b, group_size=gs, bits=nbits)
+    assert_close_bf16(orc, bits(y), ref64, what=f"qmv{nbits} gs{gs}")
+    # through the mx.gather_qmm surface (decode form: rows of one token each)
+    yg = ops.gather_qmm(bf16_t(x, dev)[:, None], words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev),
+                        lhs_indices=i32_t(xr, dev), rhs_indices=i32_t(ex, dev), group_size=gs, bits=nbits)
+    assert np.array_equal(bits(yg).reshape(R, N), bits(y))
+
+
+def test_8bit_unsupported_shapes_are_declined(dev):
+    """8-bit codes need a lane split (K <= 4096); the fused decode kernels take 4-bit only."""
+    say("8-bit declines")
+    rng = np.random.default_rng(5)
+    w, s, b = synth.quant_weights(rng, (64,), 8192, bits=8)
+    x = bf16_t(synth.bf16_bits(rng.normal(size=(1, 8192)).astype(np.float32)), dev)
+    with pytest.raises(ops.QmoeUnsupported):
+        ops.quantized_matmul(x, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), bits=8)
+    w, s, b = synth.quant_weights(rng, (4, 128), 2048, bits=8)
+    x2 = bf16_t(synth.bf16_bits(rng.normal(size=(1, 2048)).astype(np.float32)), dev)
+    with pytest.raises(ops.QmoeUnsupported):
+        ops.gate_up_silu(x2, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev),
+                         i32_t(np.zeros((1, 2), np.int32), dev), bits=8)

@@ -149,3 +149,25 @@ def test_int8_golden_is_fake_quant(orc):
     xhat = xi.astype(np.float64) * sx.astype(np.float64)[:, None]
     want = np.einsum("rk,rnk->rn", xhat, np_dequant(w, s, b)[ex])
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("bits,gs", [(8, 32), (8, 64), (8, 128), (4, 32), (4, 128)])
+@pytest.mark.parametrize("deq", ["exact", "bf16"])
+def test_gather_rows_other_widths_and_groups(orc, bits, gs, deq):
+    """8-bit codes (4 per word, low byte first) and group sizes 32 / 128
+    against the numpy shift-based dequant."""
+    rng = np.random.default_rng(bits * 1000 + gs)
+    E, N, K, R = 3, 24, 512, 11
+    w, s, b = synth.quant_weights(rng, (E, N), K, group_size=gs, bits=bits)
+    x = synth.bf16_bits(rng.normal(size=(5, K)).astype(np.float32))
+    xr = rng.integers(0, 5, size=R).astype(np.int32)
+    ex = rng.integers(0, E, size=R).astype(np.int32)
+    got, _ = orc.gather_qmm_rows(x, xr, ex, w, s, b, group_size=gs, bits=bits, deq=deq)
+    W = np_dequant(w, s, b, gs=gs, bits=bits, bf16=deq == "bf16")
+    want = np.einsum("rk,rnk->rn", xf(x)[xr], W[ex])
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    # the 8-bit byte order: a wrong (high byte first) order moves the result
+    if bits == 8:
+        swapped = ((w & 0x00FF00FF) << 8) | ((w >> 8) & 0x00FF00FF)
+        bad, _ = orc.gather_qmm_rows(x, xr, ex, swapped, s, b, group_size=gs, bits=bits, deq=deq)
+        assert np.abs(bad - want).max() > 1e-3

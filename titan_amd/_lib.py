@@ -70,6 +70,8 @@ SIGNATURES: dict[str, tuple] = {
                                           I64, P, P]),
     "qmoe_gather_qmm_int8_sorted_tiles": (INT, [P, P, P, I64, I64, P, P, I32, I64, P, P, P, P, I64, P, P]),
     "qmoe_router_topk": (INT, [P, I64, I64, I64, INT, P, P, P]),
+    "qmoe_router_logits": (INT, [P, I64, I64, P, P, P, I64, INT, INT, P, P]),
+    "qmoe_router_logits_dense": (INT, [P, I64, I64, P, I64, P, P]),
     "qmoe_gather_qmm_swiglu_sorted_tiles": (INT, [P, P, I64, I64, P, P, I32, I64, P, P, P, P, I64, P, P]),
 }
 

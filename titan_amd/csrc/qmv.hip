@@ -112,6 +112,48 @@ __device__ __forceinline__ float affine_chunk(float dq, float xsum, float s, flo
   return s * (dq - 128.0f * xsum) + b * xsum;
 }
 
+// 8-bit codes: a word holds elements 4j..4j+3, one byte each.  The nibbles of
+// bytes (0, 2) and (1, 3) go through the same bf16 magic as the 4-bit codes,
+// low and high nibble separately, so per word
+//   sum x*(128 + lo) + 16 * sum x*(128 + hi) = sum x*q + 2176 * sum x.
+// x pairs to match: p[2j] = (x[4j], x[4j+2]), p[2j+1] = (x[4j+1], x[4j+3]).
+__device__ __forceinline__ void load_x_chunk8(const uint16_t* __restrict__ src, XChunk& c) {
+  const uint4* q = reinterpret_cast<const uint4*>(src);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint4 a = q[j];
+    // words 2j (elements 8j..8j+3: a.x, a.y) and 2j+1 (8j+4..8j+7: a.z, a.w)
+    c.p[4 * j + 0] = (a.x & 0xFFFFu) | (a.y << 16);
+    c.p[4 * j + 1] = (a.x >> 16) | (a.y & 0xFFFF0000u);
+    c.p[4 * j + 2] = (a.z & 0xFFFFu) | (a.w << 16);
+    c.p[4 * j + 3] = (a.z >> 16) | (a.w & 0xFFFF0000u);
+    s += ((bf16lo(a.x) + bf16hi(a.x)) + (bf16lo(a.y) + bf16hi(a.y))) +
+         ((bf16lo(a.z) + bf16hi(a.z)) + (bf16lo(a.w) + bf16hi(a.w)));
+  }
+  c.sum = s;
+}
+
+// sum over the 32-element chunk (8 words in w0, w1) of x*(128 + lo) + 16*x*(128 + hi)
+__device__ __forceinline__ float dot_chunk8(const uint4& w0, const uint4& w1, const XChunk& c, uint32_t mv) {
+  const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  const uint32_t m = 0x000F000Fu;
+  float lo = 0.f, hi = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t v = ws[j];
+    lo = dot2_bf16(and_or(v, m, mv), c.p[2 * j + 0], lo);
+    hi = dot2_bf16(and_or(v >> 4, m, mv), c.p[2 * j + 0], hi);
+    lo = dot2_bf16(and_or(v >> 8, m, mv), c.p[2 * j + 1], lo);
+    hi = dot2_bf16(and_or(v >> 12, m, mv), c.p[2 * j + 1], hi);
+  }
+  return lo + 16.0f * hi;
+}
+
+__device__ __forceinline__ float affine_chunk8(float dq, float xsum, float s, float b) {
+  return s * (dq - 2176.0f * xsum) + b * xsum;
+}
+
 struct QmvArgs {
   const uint16_t* x;
   int64_t x_stride;      // elements between consecutive x rows
@@ -131,13 +173,15 @@ struct QmvArgs {
   const uint32_t* sb;  // tile layout: scale|bias words (w then holds the tile-layout codes)
   FastDiv blk_div;     // qmv64: blocks per pair
   FastDiv x_divf;      // qmv64: x_div
+  float* out_f32;      // plain row form only: fp32 results here instead of bf16 in out
 };
 
 // MODE 0: out[r, n] = x_row . W[e][n]
 // MODE 1: out[r, i] = silu(x_row . W[e][i]) * (x_row . W[e][n_out + i])
-template <int NV, int LPR, int MODE>
+template <int NV, int LPR, int MODE, int BITS>
 __global__ __launch_bounds__(64) void qmv_kernel(QmvArgs a) {
   constexpr int GPW = 64 / LPR;
+  constexpr int WPC = BITS / 4;  // 16-byte code loads per 32-element chunk
   const int lane = threadIdx.x;
   const int grp = lane / LPR;
   const int l = lane % LPR;
@@ -152,19 +196,24 @@ __global__ __launch_bounds__(64) void qmv_kernel(QmvArgs a) {
   const int64_t xr = a.x_rows ? (int64_t)a.x_rows[r] : r / a.x_div;
   const int K = a.K;
   const int G = K / a.group_size;
-  const int64_t KW = K / 8;
+  const int64_t KW = (int64_t)K * BITS / 32;
 
   const int64_t rg = (int64_t)e * a.n_w + nn;
-  const uint4* pg = reinterpret_cast<const uint4*>(a.w + rg * KW) + l;
-  uint4 wg[NV];
+  // chunk v of lane l: elements v*32*LPR + 32l .., loads WPC*(v*LPR + l) ..
+  const uint4* pg = reinterpret_cast<const uint4*>(a.w + rg * KW) + WPC * l;
+  uint4 wg[NV][WPC];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) wg[v] = pg[v * LPR];
-  uint4 wu[MODE == 1 ? NV : 1];
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int c = 0; c < WPC; ++c) wg[v][c] = pg[WPC * v * LPR + c];
+  uint4 wu[MODE == 1 ? NV : 1][WPC];
   const int64_t ru = rg + a.n_out;
   if (MODE == 1) {
-    const uint4* pu = reinterpret_cast<const uint4*>(a.w + ru * KW) + l;
+    const uint4* pu = reinterpret_cast<const uint4*>(a.w + ru * KW) + WPC * l;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) wu[v] = pu[v * LPR];
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+      for (int c = 0; c < WPC; ++c) wu[v][c] = pu[WPC * v * LPR + c];
   }
   float sg[NV], bg[NV], su[MODE == 1 ? NV : 1], bu[MODE == 1 ? NV : 1];
 #pragma unroll
@@ -180,21 +229,30 @@ __global__ __launch_bounds__(64) void qmv_kernel(QmvArgs a) {
   const uint16_t* xrow = a.x + xr * a.x_stride;
   XChunk xc[NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) load_x_chunk(xrow + v * 32 * LPR + l * 32, xc[v]);
+  for (int v = 0; v < NV; ++v) {
+    if (BITS == 8) load_x_chunk8(xrow + v * 32 * LPR + l * 32, xc[v]);
+    else load_x_chunk(xrow + v * 32 * LPR + l * 32, xc[v]);
+  }
 
   const uint32_t mv = magic_vgpr();
   float accg = 0.f, accu = 0.f;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    accg += affine_chunk(dot_chunk(wg[v], xc[v], mv), xc[v].sum, sg[v], bg[v]);
-    if (MODE == 1) accu += affine_chunk(dot_chunk(wu[v], xc[v], mv), xc[v].sum, su[v], bu[v]);
+    if constexpr (BITS == 8) {
+      accg += affine_chunk8(dot_chunk8(wg[v][0], wg[v][1], xc[v], mv), xc[v].sum, sg[v], bg[v]);
+      if (MODE == 1) accu += affine_chunk8(dot_chunk8(wu[v][0], wu[v][1], xc[v], mv), xc[v].sum, su[v], bu[v]);
+    } else {
+      accg += affine_chunk(dot_chunk(wg[v][0], xc[v], mv), xc[v].sum, sg[v], bg[v]);
+      if (MODE == 1) accu += affine_chunk(dot_chunk(wu[v][0], xc[v], mv), xc[v].sum, su[v], bu[v]);
+    }
   }
   accg = group_sum<LPR>(accg);
   if (MODE == 1) accu = group_sum<LPR>(accu);
   if (l == 0 && valid) {
     float o = accg;
     if (MODE == 1) o = accg / (1.0f + expf(-accg)) * accu;
-    a.out[r * a.n_out + n] = (uint16_t)f32_to_bf16(o);
+    if (MODE == 0 && a.out_f32) a.out_f32[r * a.n_out + n] = o;
+    else a.out[r * a.n_out + n] = (uint16_t)f32_to_bf16(o);
   }
 }
 
@@ -360,7 +418,10 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   } else {
     const int g = q >> 2, i = q & 3;
     const int n = (g == 0 ? n0 : grp1) + i;
-    if ((lane & 7) == 0 && i < RG && n < a.n_out) a.out[(int64_t)r * a.n_out + n] = (uint16_t)f32_to_bf16(t);
+    if ((lane & 7) == 0 && i < RG && n < a.n_out) {
+      if (a.out_f32) a.out_f32[(int64_t)r * a.n_out + n] = t;
+      else a.out[(int64_t)r * a.n_out + n] = (uint16_t)f32_to_bf16(t);
+    }
   }
 }
 
@@ -686,10 +747,10 @@ int launch_qmv64(const QmvArgs& a, dim3 grid, hipStream_t st) {
 }
 
 template <int MODE>
-int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st) {
+int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st, int bits = 4) {
   // qmv64 reads scales and biases 16 bytes at a time: G % 8 == 0 and aligned arrays
   const bool sb_ok = (a.K / a.group_size) % 8 == 0 && qmoe::aligned16(a.s) && qmoe::aligned16(a.b);
-  if (a.K % 2048 == 0 && a.K / 2048 <= 4 && (sb_ok || lpr == 0)) {
+  if (bits == 4 && a.K % 2048 == 0 && a.K / 2048 <= 4 && (sb_ok || lpr == 0)) {
     if (!sb_ok) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "scales and biases must be 16-byte aligned");
     constexpr int RG = MODE == 1 ? QMOE_QMV_RG_GU : QMOE_QMV_RG_DENSE;
     constexpr int outs = MODE == 1 ? RG : 2 * RG;
@@ -711,11 +772,18 @@ int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st) {
   if (blocks <= 0) return QMOE_OK;
   if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large (%lld blocks)", (long long)blocks);
   dim3 grid((unsigned)blocks), block(64);
-#define QMV_CASE(NV_, L_) \
-  if (nv == NV_ && lpr == L_) { qmv_kernel<NV_, L_, MODE><<<grid, block, 0, st>>>(a); return qmoe::launch_status("qmv_kernel"); }
-#define QMV_NV(L_) QMV_CASE(1, L_) QMV_CASE(2, L_) QMV_CASE(3, L_) QMV_CASE(4, L_) \
-  QMV_CASE(5, L_) QMV_CASE(6, L_) QMV_CASE(7, L_) QMV_CASE(8, L_)
-  QMV_NV(16) QMV_NV(8) QMV_NV(4)
+#define QMV_CASE(NV_, L_, B_) \
+  if (nv == NV_ && lpr == L_) { qmv_kernel<NV_, L_, MODE, B_><<<grid, block, 0, st>>>(a); return qmoe::launch_status("qmv_kernel"); }
+#define QMV_NV(L_, B_) QMV_CASE(1, L_, B_) QMV_CASE(2, L_, B_) QMV_CASE(3, L_, B_) QMV_CASE(4, L_, B_) \
+  QMV_CASE(5, L_, B_) QMV_CASE(6, L_, B_) QMV_CASE(7, L_, B_) QMV_CASE(8, L_, B_)
+  if constexpr (MODE == 0) {
+    // 8-bit codes: the plain row form only (quantized_matmul, gather_qmv)
+    if (bits == 8) {
+      QMV_NV(16, 8) QMV_NV(8, 8) QMV_NV(4, 8)
+      return qmoe::fail(QMOE_ERR_UNSUPPORTED, "no 8-bit qmv kernel for lpr=%d nv=%d", lpr, nv);
+    }
+  }
+  QMV_NV(16, 4) QMV_NV(8, 4) QMV_NV(4, 4)
 #undef QMV_NV
 #undef QMV_CASE
   return qmoe::fail(QMOE_ERR_UNSUPPORTED, "no qmv kernel for lpr=%d nv=%d", lpr, nv);
@@ -749,13 +817,17 @@ int check_tiled(int64_t K, int64_t rows_per_expert, const void* x, const void* w
   return QMOE_OK;
 }
 
-int check_common(int64_t K, int group_size, int bits, int* lpr, int* nv) {
-  if (bits != 4) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "bits=%d: only 4-bit codes have a kernel", bits);
+// allow8: the entry point has 8-bit kernels (the plain row form); they need
+// a lane split (the qmv64 fast path is 4-bit only)
+int check_common(int64_t K, int group_size, int bits, int* lpr, int* nv, bool allow8 = false) {
+  if (bits != 4 && !(allow8 && bits == 8))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "bits=%d: this entry point has %s kernels", bits,
+                      allow8 ? "4- and 8-bit" : "4-bit");
   if (group_size != 32 && group_size != 64 && group_size != 128)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "group_size=%d: kernels take 32, 64 or 128", group_size);
   if (K % group_size) return qmoe::fail(QMOE_ERR_INVALID, "K=%lld not a multiple of group_size", (long long)K);
   // K = 2048*n (n <= 4) always has the qmv64 kernel; other K need a lane split
-  const bool qmv64_ok = K % 2048 == 0 && K / 2048 <= 4;
+  const bool qmv64_ok = bits == 4 && K % 2048 == 0 && K / 2048 <= 4;
   if (!pick_split(K, lpr, nv) && !qmv64_ok)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: needs K = 32*L*n, L in {4,8,16}, n <= 8, or 2048*n, n <= 4",
                       (long long)K);
@@ -772,13 +844,13 @@ extern "C" int qmoe_gather_qmv(const uint16_t* x, const int32_t* x_rows, const i
   if (n_rows == 0) return QMOE_OK;
   if (!x || !experts || !w || !scales || !biases || !out) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
   int lpr, nv;
-  int rc = check_common(K, group_size, bits, &lpr, &nv);
+  int rc = check_common(K, group_size, bits, &lpr, &nv, true);
   if (rc) return rc;
   if (!qmoe::aligned16(x) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x and w must be 16-byte aligned");
   if (N > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N too large");
   QmvArgs a{x, K, x_rows, 1, experts, n_rows, (int)K, group_size, w, scales, biases, num_experts,
             (int)N, (int)N, out};
-  return launch_qmv<0>(a, lpr, nv, qmoe::as_stream(stream));
+  return launch_qmv<0>(a, lpr, nv, qmoe::as_stream(stream), bits);
 }
 
 extern "C" int qmoe_quantized_matmul(const uint16_t* x, int64_t M, int64_t K, const uint32_t* w,
@@ -788,12 +860,28 @@ extern "C" int qmoe_quantized_matmul(const uint16_t* x, int64_t M, int64_t K, co
   if (M == 0) return QMOE_OK;
   if (!x || !w || !scales || !biases || !out) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
   int lpr, nv;
-  int rc = check_common(K, group_size, bits, &lpr, &nv);
+  int rc = check_common(K, group_size, bits, &lpr, &nv, true);
   if (rc) return rc;
   if (!qmoe::aligned16(x) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x and w must be 16-byte aligned");
   if (N > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N too large");
   QmvArgs a{x, K, nullptr, 1, nullptr, M, (int)K, group_size, w, scales, biases, 1, (int)N, (int)N, out};
-  return launch_qmv<0>(a, lpr, nv, qmoe::as_stream(stream));
+  return launch_qmv<0>(a, lpr, nv, qmoe::as_stream(stream), bits);
+}
+
+extern "C" int qmoe_router_logits(const uint16_t* x, int64_t T, int64_t K, const uint32_t* w,
+                                  const uint16_t* scales, const uint16_t* biases, int64_t E, int group_size,
+                                  int bits, float* logits, void* stream) {
+  if (T < 0 || E <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (T == 0) return QMOE_OK;
+  if (!x || !w || !scales || !biases || !logits) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  int lpr, nv;
+  int rc = check_common(K, group_size, bits, &lpr, &nv, true);
+  if (rc) return rc;
+  if (!qmoe::aligned16(x) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x and w must be 16-byte aligned");
+  if (E > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "E too large");
+  QmvArgs a{x, K, nullptr, 1, nullptr, T, (int)K, group_size, w, scales, biases, 1, (int)E, (int)E, nullptr};
+  a.out_f32 = logits;
+  return launch_qmv<0>(a, lpr, nv, qmoe::as_stream(stream), bits);
 }
 
 extern "C" int qmoe_moe_gate_up_swiglu(const uint16_t* x, const int32_t* idx, int64_t T,

@@ -96,7 +96,64 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
   }
 }
 
+// Router logits over a dense bf16 router weight: logits[t, e] = x[t] . W[e]
+// in fp32 (v_dot2_f32_bf16), one wave per (token, expert) row, each lane
+// taking 16-byte units u = lane, lane + 64, ... of both rows.
+__global__ __launch_bounds__(256) void router_logits_dense_kernel(const uint16_t* __restrict__ x, int64_t T,
+                                                                 int K, const uint16_t* __restrict__ w, int E,
+                                                                 float* __restrict__ logits) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  if (row >= T * E) return;
+  const int64_t t = row / E;
+  const int64_t e = row - t * E;
+  const uint4* xp = reinterpret_cast<const uint4*>(x + t * K);
+  const uint4* wp = reinterpret_cast<const uint4*>(w + e * K);
+  const int units = K / 8;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int u = lane;
+  for (; u + 192 < units; u += 256) {  // four units in flight per lane
+    uint4 xv[4], wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xv[j] = xp[u + 64 * j];
+      wv[j] = wp[u + 64 * j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[j] = dot2_bf16(xv[j].x, wv[j].x, acc[j]);
+      acc[j] = dot2_bf16(xv[j].y, wv[j].y, acc[j]);
+      acc[j] = dot2_bf16(xv[j].z, wv[j].z, acc[j]);
+      acc[j] = dot2_bf16(xv[j].w, wv[j].w, acc[j]);
+    }
+  }
+  for (; u < units; u += 64) {
+    const uint4 xv = xp[u], wv = wp[u];
+    acc[0] = dot2_bf16(xv.x, wv.x, acc[0]);
+    acc[0] = dot2_bf16(xv.y, wv.y, acc[0]);
+    acc[0] = dot2_bf16(xv.z, wv.z, acc[0]);
+    acc[0] = dot2_bf16(xv.w, wv.w, acc[0]);
+  }
+  const float v = wave_sum((acc[0] + acc[1]) + (acc[2] + acc[3]));
+  if (lane == 0) logits[row] = v;
+}
+
 }  // namespace
+
+extern "C" int qmoe_router_logits_dense(const uint16_t* x, int64_t T, int64_t K, const uint16_t* w, int64_t E,
+                                        float* logits, void* stream) {
+  if (T < 0 || K <= 0 || E <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (T == 0) return QMOE_OK;
+  if (!x || !w || !logits) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (K % 8) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: must be a multiple of 8", (long long)K);
+  if (K > 0x7FFFFFFF || E > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
+  if (!qmoe::aligned16(x) || !qmoe::aligned16(w)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x and w must be 16-byte aligned");
+  const int64_t blocks = (T * E + 3) / 4;
+  if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "too many rows");
+  router_logits_dense_kernel<<<dim3((unsigned)blocks), dim3(256), 0, qmoe::as_stream(stream)>>>(x, T, (int)K, w,
+                                                                                               (int)E, logits);
+  return qmoe::launch_status("router_logits_dense_kernel");
+}
 
 extern "C" int qmoe_router_topk(const float* logits, int64_t T, int64_t E, int64_t k, int norm, int32_t* idx,
                                 float* scores, void* stream) {

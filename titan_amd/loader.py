@@ -16,7 +16,9 @@ reference (loader.py:1-31):
   (``concatenate([gate, up], axis=1)`` over weight, scales and biases alike:
   exact, because affine groups run along the input axis; loader.py:19-27,
   244-262) and builds a :class:`~titan_amd.moe_block.SparseMoeBlock`, whose
-  constructor repacks the prefill copies into the tile layout once.
+  constructor repacks the prefill copies into the tile layout once.  A
+  quantised router stays quantised (its decode logits come from the codes);
+  a quantised shared-expert gate is dequantised.
 
 The header format is the published safetensors one: an 8-byte little-endian
 header length, a JSON header mapping each tensor name to ``dtype``, ``shape``
@@ -328,7 +330,12 @@ def load_moe_block(model_dir, prefix: str | None = None, device="cuda", *, tenso
                          f"({spec} vs {plan.quant[f'{prefix}.switch_mlp.down_proj']})")
     t = load_moe_tensors(tensors, plan, device)
     gu, dn = _with_biases(t["gate_up"]), _with_biases(t["down"])
-    router = _dense(tensors, plan.router, device, plan.quant.get(f"{prefix}.gate"))
+    rspec = plan.quant.get(f"{prefix}.gate") or spec
+    if "scales" in plan.router:  # kept quantised: the decode logits come from the codes
+        router = _with_biases(tuple(read_tensor(tensors[plan.router[s]]).to(device) if s in plan.router else None
+                                    for s in QUANT_SUFFIXES))
+    else:
+        router = _dense(tensors, plan.router, device, None)
     shared = None
     if plan.shared:
         sspec = plan.quant[f"{prefix}.shared_expert.gate_proj"]
@@ -342,7 +349,8 @@ def load_moe_block(model_dir, prefix: str | None = None, device="cuda", *, tenso
     norm = bool(text.get("norm_topk_prob", True))
     return moe_block.SparseMoeBlock(router, gu, dn, top_k, norm_topk_prob=norm, wsum_mode=wsum_mode,
                                     group_size=spec["group_size"], bits=spec["bits"], shared=shared,
-                                    prefill_tiles=prefill_tiles)
+                                    prefill_tiles=prefill_tiles,
+                                    router_quant=(rspec["group_size"], rspec["bits"]))
 
 
 def _with_biases(trio):

@@ -3,7 +3,8 @@
 Qwen3_5MoeSparseMoeBlock.__call__, with the fused router of
 engine/patches/decode-fusion/fused_kernels.py:232-371).
 
-    logits  = x @ W_router^T                         fp32 (library GEMM)
+    logits  = x @ W_router^T, fp32                   qmoe_router_logits[_dense] (T <= 16),
+                                                     else a library fp32 GEMM
     idx, sc = top-k of logits, softmax over the k    qmoe_router_topk
     decode  (T * k < 64, switch_layers.py:218):
         h   = silu(x W_gate^T) * (x W_up^T)          qmoe_moe_gate_up_swiglu
@@ -32,10 +33,12 @@ import torch
 
 from . import ops
 
-__all__ = ["SparseMoeBlock", "SharedExpert", "DECODE_MAX_PAIRS"]
+__all__ = ["SparseMoeBlock", "SharedExpert", "DECODE_MAX_PAIRS", "ROUTER_GEMV_MAX_T"]
 
 # switch_layers.py:218: SwitchGLU sorts when indices.size >= 64
 DECODE_MAX_PAIRS = 64
+# router logits through the GEMV kernels up to this many tokens, a GEMM above
+ROUTER_GEMV_MAX_T = 16
 
 
 @dataclass
@@ -52,16 +55,33 @@ class SharedExpert:
 class SparseMoeBlock:
     """Routed experts of one MoE layer over MLX-affine 4-bit weights.
 
-    ``router_weight`` bf16 [E, H]; ``gate_up`` = (w, scales, biases) of the
+    ``router_weight`` bf16 [E, H], or an affine-quantized (w, scales, biases)
+    triple with ``router_quant = (group_size, bits)`` whose decode logits come
+    straight from the codes (the fused router, fused_kernels.py:232-260);
+    ``gate_up`` = (w, scales, biases) of the
     fused [E, 2I, H] projection (gate rows first, loader.py:19-27); ``down`` =
     (w, scales, biases) of [E, H, I].  The prefill copies of both weights are
     repacked into the tile layout once, here (the gate_up copy in the
-    gate/up-paired row order of the SwiGLU GEMM)."""
+    gate/up-paired row order of the SwiGLU GEMM).
+
+    ``sort_min_pairs`` is where the sorted path takes over (default 64, stock
+    SwitchGLU's rule).  The two paths round differently -- the decode kernels
+    use the exact affine weights, the grouped GEMMs bf16-materialised ones,
+    as MLX's qmv and qmm do -- so the default keeps stock's numerics; a
+    larger value trades that for speed at mid widths, where the decode
+    kernels are faster on this part."""
 
     def __init__(self, router_weight: torch.Tensor, gate_up: tuple, down: tuple, top_k: int,
                  norm_topk_prob: bool = True, wsum_mode: str = "fast", group_size: int = ops.GROUP,
-                 bits: int = ops.BITS, shared: SharedExpert | None = None, prefill_tiles: bool = True):
-        self.router_weight = router_weight
+                 bits: int = ops.BITS, shared: SharedExpert | None = None, prefill_tiles: bool = True,
+                 sort_min_pairs: int = DECODE_MAX_PAIRS, router_quant: tuple = (ops.GROUP, ops.BITS)):
+        self.router_weight = router_weight if isinstance(router_weight, torch.Tensor) else tuple(router_weight)
+        self.router_quant = tuple(router_quant)
+        if isinstance(self.router_weight, torch.Tensor):
+            dense = self.router_weight
+        else:  # prefill logits: a GEMM over the weights dequantised once (bf16(fma(q, s, b)))
+            dense = ops.dequantize(*self.router_weight, *self.router_quant)
+        self._router_f32 = dense.float().contiguous()
         self.gate_up = tuple(gate_up)
         self.down = tuple(down)
         self.top_k = int(top_k)
@@ -75,6 +95,9 @@ class SparseMoeBlock:
         if prefill_tiles:
             self.gu_tiles = ops.repack_tiles(*self.gate_up, group_size, bits, swiglu_pairs=True)
             self.down_tiles = ops.repack_tiles(*self.down, group_size, bits)
+        # the sorted (grouped GEMM) path from this many (token, expert) pairs
+        # on; below it the decode kernels (which take at most 16 tokens)
+        self.sort_min_pairs = int(sort_min_pairs)
         self.shared = shared
         self._shared_tiles = None
         if shared is not None and prefill_tiles:
@@ -82,17 +105,27 @@ class SparseMoeBlock:
                                   ops.repack_tiles(*shared.down, group_size, bits))
 
     # ------------------------------------------------------------- router
+    def route_logits(self, x2: torch.Tensor) -> torch.Tensor:
+        """fp32 router logits [T, E] for tokens x2 [T, H]."""
+        if x2.shape[0] <= ROUTER_GEMV_MAX_T:
+            return ops.router_logits(x2, self.router_weight, *self.router_quant)
+        return torch.matmul(x2.float(), self._router_f32.t())
+
     def route(self, x2: torch.Tensor):
         """(idx int32 [T, k], scores fp32 [T, k]) for tokens x2 [T, H]."""
-        logits = torch.matmul(x2.float(), self.router_weight.float().t())
-        return ops.router_topk(logits, self.top_k, self.norm)
+        return ops.router_topk(self.route_logits(x2), self.top_k, self.norm)
 
     # ------------------------------------------------------------- experts
     def experts(self, x2: torch.Tensor, idx: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
         """sum_j scores[t, j] * expert_{idx[t, j]}(x2[t]) for x2 [T, H]."""
         T = x2.shape[0]
         k = idx.shape[-1]
-        if T * k < DECODE_MAX_PAIRS or self.gu_tiles is None:
+        decode = T * k < self.sort_min_pairs and T <= 16
+        if not decode and self.gu_tiles is None:
+            if T > 16:
+                raise ValueError("block built with prefill_tiles=False takes decode widths only (T <= 16)")
+            decode = True
+        if decode:
             h = ops.gate_up_silu(x2, *self.gate_up, idx, self.group_size, self.bits)
             return ops.down_wsum(h, *self.down, idx, scores, self.group_size, self.bits)
         r = ops.route(idx, self.num_experts)
@@ -115,8 +148,11 @@ class SparseMoeBlock:
             tiles = ops.build_tiles(zeros.reshape(-1), 1)
             h = ops.gather_qmm_swiglu_sorted_tiles(x2, gu_t, tiles)
             y = ops.gather_qmm_sorted_tiles(h, dn_t, tiles)
-        g = torch.sigmoid(torch.matmul(x2.float(), sh.gate_weight.float().t()))
-        return (g * y.float()).to(torch.bfloat16)
+        if T <= ROUTER_GEMV_MAX_T:
+            z = ops.router_logits(x2, sh.gate_weight)
+        else:
+            z = torch.matmul(x2.float(), sh.gate_weight.float().t())
+        return (torch.sigmoid(z) * y.float()).to(torch.bfloat16)
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         H = x.shape[-1]

@@ -607,9 +607,34 @@ def router_topk(logits: torch.Tensor, k: int, norm: bool = True):
     return idx.reshape(*lg.shape[:-1], k), scores.reshape(*lg.shape[:-1], k)
 
 
+def router_logits(x: torch.Tensor, router, group_size: int = GROUP, bits: int = BITS) -> torch.Tensor:
+    """fp32 router logits [T, E] for tokens x [T, K]: ``router`` a dense bf16
+    [E, K] weight, or an affine-quantized (w, scales, biases) triple, whose
+    logits come straight from the codes (decode-fusion/fused_kernels.py:232-260)."""
+    x = _bf16(x, "x")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    T = x2.shape[0]
+    if isinstance(router, torch.Tensor):
+        w = _bf16(router, "router")
+        E = w.shape[0]
+        out = torch.empty(T, E, dtype=torch.float32, device=x.device)
+        _lib.call("qmoe_router_logits_dense", x2.data_ptr(), T, K, w.data_ptr(), E, out.data_ptr(), _stream(x))
+        return out
+    w, scales, biases = _words(router[0], "w"), _bf16(router[1], "scales"), _bf16(router[2], "biases")
+    if w.dim() != 2:
+        raise QmoeUnsupported(_lib.ERR_UNSUPPORTED, f"router w must be [E, K*bits/32], got {tuple(w.shape)}")
+    _check_quant(w, scales, group_size, bits, K)
+    E = w.shape[0]
+    out = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    _lib.call("qmoe_router_logits", x2.data_ptr(), T, K, w.data_ptr(), scales.data_ptr(), biases.data_ptr(), E,
+              group_size, bits, out.data_ptr(), _stream(x))
+    return out
+
+
 __all__ = [
     "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "TileWeights", "Routing", "build_tiles", "route",
-    "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmm_int8_sorted_tiles", "router_topk", "gather_qmm_swiglu_sorted_tiles", "swiglu_pair_order", "gather_qmv_tiles", "gate_up_silu_tiles",
+    "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmm_int8_sorted_tiles", "router_topk", "router_logits", "gather_qmm_swiglu_sorted_tiles", "swiglu_pair_order", "gather_qmv_tiles", "gate_up_silu_tiles",
     "max_tiles", "tile_rows", "unpack", "dequantize", "gather_qmv", "gather_qmm_sorted", "gather_qmm",
     "gemm_supported", "quantized_matmul", "gate_up_silu", "down_wsum", "moe_weighted_sum",
     "quantize_act_int8", "gather_qmm_int8_sorted",

@@ -5,9 +5,9 @@ The reference leaves these shapes on MLX's own gather_qmv
 (titan/adapters/mlx/compiled.py:490-518, 209-218); this overlay is their
 drop-in.  Routed when: ``sorted_indices`` false, affine ``transpose=True``
 weights with biases, bf16 activations on the GPU.  Shapes the kernels do not
-take (bits other than 4, group sizes other than 32/64/128, K outside the
-kernels' range) raise :class:`~titan_amd._lib.QmoeUnsupported` inside the route
-and are handed down.
+take (bits other than 4 and 8, group sizes other than 32/64/128, K outside the
+kernels' range: 8-bit codes up to K = 4096) raise
+:class:`~titan_amd._lib.QmoeUnsupported` inside the route and are handed down.
 
     TITAN_AMD_MOE_DECODE=1   enable (default on)
 """

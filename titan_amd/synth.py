@@ -97,7 +97,7 @@ class Workload:
 
 def make(cfg: int, seed: int | None = None, *, tokens: int | None = None,
          experts: int = EXPERTS) -> Workload:
-    """Build workload ``cfg`` (0..4).  ``tokens`` shrinks the prefill workloads
+    """Build workload ``cfg`` (0..4; 5: workload 0 with 8-bit codes).  ``tokens`` shrinks the prefill workloads
     for tests; ``experts`` shrinks E (the ids stay in range)."""
     seed = cfg if seed is None else seed
     rng = rng_for(seed)
@@ -131,6 +131,10 @@ def make(cfg: int, seed: int | None = None, *, tokens: int | None = None,
             x = np.where(out, x * 20.0, x).astype(np.float32)
         A["x"] = bf16_bits(x)
         M.update(T=T, k=TOP_K, K=HIDDEN, N=2 * INTER, E=experts)
+    elif cfg == 5:
+        A["w"], A["s"], A["b"] = quant_weights(rng, (4096,), HIDDEN, bits=8)
+        A["x"] = bf16_bits(rng.normal(0.0, 1.0, size=(1, HIDDEN)).astype(np.float32))
+        M.update(M=1, N=4096, K=HIDDEN, bits=8)
     else:
         raise ValueError(f"no workload {cfg}")
     return wl
@@ -141,6 +145,8 @@ def algorithmic_bytes(cfg: int, wl: Workload | None = None) -> int:
     row_bytes = lambda K: K // 2 + (K // GROUP) * 4  # packed codes + bf16 scale & bias
     if cfg == 0:
         return 4096 * row_bytes(HIDDEN) + HIDDEN * 2 + 4096 * 2
+    if cfg == 5:  # 8-bit codes: one byte per element
+        return 4096 * (HIDDEN + (HIDDEN // GROUP) * 4) + HIDDEN * 2 + 4096 * 2
     if cfg == 1:
         return TOP_K * 2 * INTER * row_bytes(HIDDEN) + HIDDEN * 2 + TOP_K * INTER * 2 * 2
     if cfg == 2:
@@ -152,7 +158,7 @@ def algorithmic_bytes(cfg: int, wl: Workload | None = None) -> int:
 
 
 def algorithmic_flops(cfg: int, wl: Workload | None = None) -> int:
-    if cfg == 0:
+    if cfg in (0, 5):
         return 2 * 4096 * HIDDEN
     if cfg == 1:
         return 2 * TOP_K * 2 * INTER * HIDDEN
