@@ -388,7 +388,7 @@ def setup_cfg2(args, dev):
     bytes_ = int(mean_distinct * 2048 * row_bytes + 8 * 10 * 512 * 2 + 8 * 2048 * 2 + 8 * 10 * 4)
     return wl, [mk(i) for i in range(args.steps)], {
         "bytes": bytes_, "flops": synth.algorithmic_flops(2, wl), "bound": "hbm",
-        "kernel": "down512_kernel<8>", "sets": len(sets), "mean_distinct_experts": mean_distinct,
+        "kernel": "down_pair_kernel<16>", "sets": len(sets), "mean_distinct_experts": mean_distinct,
         "workload": "decode down + top-10 weighted sum: 8 tokens, I=512, D=2048, E=256, "
                     "W [256,2048,512] int4 g64 -> y [8,2048]"}
 

@@ -31,10 +31,6 @@ constexpr uint32_t kMagic = 0x43004300u;  // bf16 128.0 in both halves
 #ifndef QMOE_QMV_RG_DENSE
 #define QMOE_QMV_RG_DENSE 2
 #endif
-// Rows per wave of the I = 512 fused down kernel (a multiple of 4).
-#ifndef QMOE_DOWN_ROWS
-#define QMOE_DOWN_ROWS 8
-#endif
 
 // x pairs laid out to match the nibble pairs of one 32-bit code word:
 // word j covers elements 8j..8j+7; pairs are (0,4), (1,5), (2,6), (3,7).
@@ -578,122 +574,61 @@ __global__ __launch_bounds__(1024) void down_wsum_kernel(DownArgs a) {
   if (l == 0 && valid) a.y[(int64_t)t * a.D + d] = (uint16_t)f32_to_bf16(acc);
 }
 
-// Fused down + weighted sum for I = 512 (one 32-code chunk per lane and row).
-// A block holds W waves of one token t; wave w covers rows
-// d0 = (blockIdx.x*W + w)*R .. d0 + R - 1 of every expert of that token, lane
-// (rg = lane/16, l = lane%16) owning chunk l of rows d0 + 4i + rg (i < R/4),
-// so each 16-byte load instruction reads four consecutive 256-byte rows.
-//  * Loads of all of the token's (up to kDownMaxK) experts are issued before
-//    any arithmetic: the codes and scales are one dependent round trip after
-//    the expert ids, with nothing batched behind them.
-//  * The token's k rows of h are turned into x pairs and 32-element sums once
-//    per block, in LDS ([expert][pair quad][chunk] 16-byte units, read
-//    conflict-free), instead of once per wave and expert.
-//  * The router score is folded into the per-lane partial; one 16-lane
-//    reduction per row ends the weighted sum (fused_kernels.py:93-169).
-// Tokens that share an expert read its rows from L2 or the Infinity Cache.
-constexpr int kDownMaxK = 12;
-constexpr int kDownWaves = 4;  // waves per block
+// Fused down + weighted sum for I = 512, pair-parallel: one block per
+// (token t, R output rows), one wave per expert slot j of the token (k waves).
+// Lane (rg = lane/16, l = lane%16) owns 32-code chunk l of rows d0 + 4i + rg
+// (i < R/4), so each 16-byte load instruction reads four consecutive 256-byte
+// rows.  A wave streams only its own expert's R rows (R * 288 bytes), which
+// puts k waves per row block in flight: at one token, 2560 waves where a wave
+// per (token, row block) walking all k experts gives 256 and is latency-bound.
+// The pair's h chunk is loaded before the expert id (it does not depend on
+// it); the slots' score-weighted row values meet in LDS and are summed in
+// slot order, so the result is deterministic (fused_kernels.py:93-169
+// arithmetic: fp32 throughout, one bf16 rounding).  Tokens that share an
+// expert read its rows from L2 or the Infinity Cache.
+constexpr int kPairMaxK = 16;
 
 template <int R>
-__global__ __launch_bounds__(64 * kDownWaves) void down512_kernel(DownArgs a) {
+__global__ __launch_bounds__(64 * kPairMaxK) void down_pair_kernel(DownArgs a) {
   constexpr int NI = R / 4;
-  __shared__ uint4 hp[kDownMaxK][5][16];  // pair words 4q..4q+3 in [j][q][l]; [j][4][l].x = chunk sum
+  __shared__ float red[kPairMaxK][R];
   const int t = blockIdx.y;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  constexpr int W = kDownWaves;
+  const int j = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int rg = lane >> 4, l = lane & 15;
-  const int d0 = (blockIdx.x * W + w) * R;
-  const int k = a.k, D = a.D;
+  const int d0 = blockIdx.x * R;
+  const int D = a.D;
   const int G = 512 / a.group_size;
   const int gi = (l * 32) / a.group_size;
-  const int64_t pbase = (int64_t)t * k;
-
-  // h chunks this thread formats (k*16 items over the block)
-  const int nitems = k * 16;
-  constexpr int kItemsMax = (kDownMaxK * 16 + 64 * W - 1) / (64 * W);
-  uint4 hv[kItemsMax][4];
-#pragma unroll
-  for (int it = 0; it < kItemsMax; ++it) {
-    const int item = threadIdx.x + it * 64 * W;
-    if (item < nitems) {
-      const uint4* src = reinterpret_cast<const uint4*>(a.h + (pbase + item / 16) * 512 + (item % 16) * 32);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) hv[it][q] = src[q];
-    }
-  }
-
-  uint4 wq[kDownMaxK][NI];
-  uint16_t sv[kDownMaxK][NI], bv[kDownMaxK][NI];
-  float sc[kDownMaxK];
-#pragma unroll
-  for (int j = 0; j < kDownMaxK; ++j) {
-    if (j < k) {
-      int e = a.idx[pbase + j];
-      e = min(max(e, 0), a.num_experts - 1);
-      sc[j] = a.scores[pbase + j];
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int64_t row = (int64_t)e * D + min(d0 + 4 * i + rg, D - 1);
-        wq[j][i] = load_nt(reinterpret_cast<const uint4*>(a.w + row * 64) + l);
-        sv[j][i] = a.s[row * G + gi];
-        bv[j][i] = a.b[row * G + gi];
-      }
-    }
-  }
-
-#pragma unroll
-  for (int it = 0; it < kItemsMax; ++it) {
-    const int item = threadIdx.x + it * 64 * W;
-    if (item < nitems) {
-      const int j = item / 16, c = item % 16;
-      uint32_t p[16];
-      float s = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint4 v = hv[it][q];
-        p[4 * q + 0] = (v.x & 0xFFFFu) | (v.z << 16);
-        p[4 * q + 1] = (v.x >> 16) | (v.z & 0xFFFF0000u);
-        p[4 * q + 2] = (v.y & 0xFFFFu) | (v.w << 16);
-        p[4 * q + 3] = (v.y >> 16) | (v.w & 0xFFFF0000u);
-        s += ((bf16lo(v.x) + bf16hi(v.x)) + (bf16lo(v.y) + bf16hi(v.y))) +
-             ((bf16lo(v.z) + bf16hi(v.z)) + (bf16lo(v.w) + bf16hi(v.w)));
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) hp[j][q][c] = make_uint4(p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]);
-      hp[j][4][c] = make_uint4(__float_as_uint(s), 0u, 0u, 0u);
-    }
-  }
-  __syncthreads();
-
-  const uint32_t mv = magic_vgpr();
-  float acc[NI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) acc[i] = 0.f;
-#pragma unroll
-  for (int j = 0; j < kDownMaxK; ++j) {
-    if (j < k) {
-      XChunk hc;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint4 u = hp[j][q][l];
-        hc.p[4 * q] = u.x;
-        hc.p[4 * q + 1] = u.y;
-        hc.p[4 * q + 2] = u.z;
-        hc.p[4 * q + 3] = u.w;
-      }
-      hc.sum = __uint_as_float(hp[j][4][l].x);
-#pragma unroll
-      for (int i = 0; i < NI; ++i)
-        acc[i] += sc[j] * affine_chunk(dot_chunk(wq[j][i], hc, mv), hc.sum, bf16_to_f32(sv[j][i]),
-                                       bf16_to_f32(bv[j][i]));
-    }
-  }
+  const int64_t p = (int64_t)t * a.k + j;
+  // the pair's h chunk first: it does not wait for the expert id
+  XChunk hc;
+  load_x_chunk(a.h + p * 512 + l * 32, hc);
+  int e = a.idx[p];
+  e = min(max(e, 0), a.num_experts - 1);
+  const float sc = a.scores[p];
+  uint4 wq[NI];
+  uint16_t sv[NI], bv[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const float v = group_sum<16>(acc[i]);
-    const int d = d0 + 4 * i + rg;
-    if (l == 0 && d < D) a.y[(int64_t)t * D + d] = (uint16_t)f32_to_bf16(v);
+    const int64_t row = (int64_t)e * D + min(d0 + 4 * i + rg, D - 1);
+    wq[i] = load_nt(reinterpret_cast<const uint4*>(a.w + row * 64) + l);
+    sv[i] = a.s[row * G + gi];
+    bv[i] = a.b[row * G + gi];
+  }
+  const uint32_t mv = magic_vgpr();
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const float v = group_sum<16>(affine_chunk(dot_chunk(wq[i], hc, mv), hc.sum, bf16_to_f32(sv[i]),
+                                               bf16_to_f32(bv[i])));
+    if (l == 0) red[j][4 * i + rg] = sc * v;
+  }
+  __syncthreads();
+  if (threadIdx.x < R) {
+    float y = 0.f;
+    for (int jj = 0; jj < a.k; ++jj) y += red[jj][threadIdx.x];
+    const int d = d0 + threadIdx.x;
+    if (d < D) a.y[(int64_t)t * D + d] = (uint16_t)f32_to_bf16(y);
   }
 }
 
@@ -921,14 +856,14 @@ extern "C" int qmoe_moe_down_wsum(const uint16_t* h, const int32_t* idx, const f
   DownArgs a{h, idx, scores, (int)T, (int)top_k, (int)I, group_size, w, scales, biases,
              num_experts, (int)D, y};
   hipStream_t st = qmoe::as_stream(stream);
-  if (I == 512 && top_k <= kDownMaxK && qmoe::aligned16(h)) {
-    // blocks of kDownWaves waves of one token, R rows per wave
-    constexpr int R = QMOE_DOWN_ROWS;
-    const int64_t waves_per_token = (D + R - 1) / R;
-    dim3 grid2((unsigned)((waves_per_token + kDownWaves - 1) / kDownWaves), (unsigned)T),
-        block2(64 * kDownWaves);
-    down512_kernel<R><<<grid2, block2, 0, st>>>(a);
-    return qmoe::launch_status("down512_kernel");
+  if (I == 512 && top_k <= kPairMaxK) {
+    // rows per wave: 8 for one token (more waves in flight), 16 from two on
+    // (measured: 3.6 vs 4.5 us at T = 1, 11.6 vs 14.9 us at T = 8)
+    const int R = T == 1 ? 8 : 16;
+    dim3 grid2((unsigned)((D + R - 1) / R), (unsigned)T), block2((unsigned)(64 * top_k));
+    if (R == 8) down_pair_kernel<8><<<grid2, block2, 0, st>>>(a);
+    else down_pair_kernel<16><<<grid2, block2, 0, st>>>(a);
+    return qmoe::launch_status("down_pair_kernel");
   }
   const int gpw = 64 / lpr;
   dim3 grid((unsigned)((D + gpw - 1) / gpw)), block((unsigned)(64 * T));
