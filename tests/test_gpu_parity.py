@@ -54,9 +54,13 @@ def _route_cases():
     yield "uniform", rng.integers(0, 32, size=200).astype(np.int32), 32
     yield "single", np.array([3], np.int32), 8
     yield "ragged", rng.integers(0, 1000, size=12345).astype(np.int32), 1000
+    # the single-block path takes up to 8192 pairs and 512 experts
+    yield "fused-max", rng.integers(0, 512, size=8192).astype(np.int32), 512
+    yield "split-min", rng.integers(0, 512, size=8193).astype(np.int32), 512
+    yield "zipf-700", synth.make(3, tokens=700)["idx"], 256
 
 
-@pytest.mark.parametrize("case", list(range(5)))
+@pytest.mark.parametrize("case", list(range(8)))
 def test_route_matches_stable_sort(dev, orc, case):
     name, ids, E = list(_route_cases())[case]
     say(f"route {name} n={ids.size} E={E}")
@@ -74,11 +78,14 @@ def test_route_matches_stable_sort(dev, orc, case):
     assert int(r.bad_ids.item()) == 0
 
 
-def test_route_clamps_out_of_range_ids(dev, orc):
-    say("route out-of-range ids")
+@pytest.mark.parametrize("n", [7, 9000])
+def test_route_clamps_out_of_range_ids(dev, orc, n):
+    say(f"route out-of-range ids n={n}")
     ids = np.array([0, 5, 9, -1, 3, 12, 5], np.int32)
+    if n > ids.size:
+        ids = np.concatenate([ids, np.random.default_rng(n).integers(-2, 10, size=n - ids.size).astype(np.int32)])
     r = ops.route(i32_t(ids, dev), 8)
-    assert int(r.bad_ids.item()) == 3
+    assert int(r.bad_ids.item()) == int(((ids < 0) | (ids >= 8)).sum())
     clamped = np.clip(ids, 0, 7)
     order, inv, srt = orc.route_sort(clamped, 8)
     assert np.array_equal(r.order.cpu().numpy(), order)

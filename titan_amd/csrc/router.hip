@@ -13,7 +13,8 @@
 //
 // Lane l holds experts l, l + 64, ... (PER per lane, coalesced loads).  Each
 // round takes the wave maximum of the lanes' best untaken values, then the
-// lowest expert index holding it, and retires that expert in its owner lane.
+// lowest expert index holding it (one ballot per column of 64 experts), and
+// retires that expert in its owner lane.
 #include <limits.h>
 
 #include "common.h"
@@ -23,20 +24,35 @@ namespace {
 constexpr int kMaxK = 64;
 constexpr int kMaxPer = 16;  // E <= 1024
 
+// Whole-wave reductions that leave the result in every lane, without the
+// LDS crossbar (__shfl_xor lowers to ds_bpermute, whose latency dominated a
+// k-round top-k): two quad_perm steps, row_half_mirror and row_ror:8 cover a
+// 16-lane row with DPP, then v_permlane16_swap and v_permlane32_swap combine
+// the rows.
+template <class Op>
+__device__ __forceinline__ float wave_all(float v, Op op) {
+  auto dpp = [](float x, int ctrl) {
+    switch (ctrl) {  // the control word must be a constant
+      case 0xB1: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0xB1, 0xf, 0xf, false));
+      case 0x4E: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x4E, 0xf, 0xf, false));
+      case 0x141: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x141, 0xf, 0xf, false));
+      default: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x128, 0xf, 0xf, false));
+    }
+  };
+  v = op(v, dpp(v, 0xB1));   // quad_perm 1,0,3,2
+  v = op(v, dpp(v, 0x4E));   // quad_perm 2,3,0,1
+  v = op(v, dpp(v, 0x141));  // row_half_mirror
+  v = op(v, dpp(v, 0x128));  // row_ror:8
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  return wave_all(v, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-__device__ __forceinline__ int wave_min(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m, 64));
-  return v;
+  return wave_all(v, [](float a, float b) { return a + b; });
 }
 
 template <int PER>
@@ -71,23 +87,27 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
   float mine = -INFINITY;  // lane j keeps the j-th chosen logit
   for (int j = 0; j < k; ++j) {
     float bv = -INFINITY;
-    int bc = -1;
 #pragma unroll
     for (int c = 0; c < PER; ++c)
-      if (!(taken >> c & 1) && (bc < 0 || v[c] > bv)) {
-        bv = v[c];
-        bc = c;
+      if (!(taken >> c & 1)) bv = fmaxf(bv, v[c]);
+    const float wm = wave_max(bv);
+    // the lowest expert index holding the maximum: column c = e / 64 first,
+    // then the lowest lane of that column (one ballot per column)
+    int sel = 0;  // no comparable candidate (NaN logits): stay in range
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const uint64_t m = __ballot(!(taken >> c & 1) && v[c] == wm);
+      if (m) {
+        sel = 64 * c + __builtin_ctzll(m);
+        break;
       }
-    const float wm = wave_max(bc >= 0 ? bv : -INFINITY);
-    const int cand = (bc >= 0 && bv == wm) ? bc * 64 + lane : INT_MAX;
-    int sel = wave_min(cand);
-    if (sel == INT_MAX) sel = 0;  // no comparable candidate (NaN logits): stay in range
-    if (cand == sel) taken |= 1u << bc;
+    }
+    if (lane == (sel & 63)) taken |= 1u << (sel >> 6);
     if (lane == 0) idx[t * k + j] = sel;
     if (lane == j) mine = wm;
   }
   if (norm) {
-    const float top0 = __shfl(mine, 0, 64);
+    const float top0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(mine), 0));
     const float p = lane < k ? expf(mine - top0) : 0.f;
     const float denom = wave_sum(p);
     if (lane < k) scores[t * k + lane] = p / denom;
