@@ -4,7 +4,7 @@ Qwen3_5MoeSparseMoeBlock.__call__, with the fused router of
 engine/patches/decode-fusion/fused_kernels.py:232-371).
 
     logits  = x @ W_router^T, fp32                   qmoe_router_logits[_dense] (T <= 16),
-                                                     else a library fp32 GEMM
+                                                     else a library bf16 GEMM, fp32 out
     idx, sc = top-k of logits, softmax over the k    qmoe_router_topk
     decode  (T * k < 64, switch_layers.py:218):
         h   = silu(x W_gate^T) * (x W_up^T)          qmoe_moe_gate_up_swiglu
@@ -78,10 +78,11 @@ class SparseMoeBlock:
         self.router_weight = router_weight if isinstance(router_weight, torch.Tensor) else tuple(router_weight)
         self.router_quant = tuple(router_quant)
         if isinstance(self.router_weight, torch.Tensor):
-            dense = self.router_weight
+            dense = self.router_weight.to(torch.bfloat16)
         else:  # prefill logits: a GEMM over the weights dequantised once (bf16(fma(q, s, b)))
             dense = ops.dequantize(*self.router_weight, *self.router_quant)
-        self._router_f32 = dense.float().contiguous()
+        # [H, E] contiguous: the library GEMM gets no transposed view
+        self._router_dense_t = dense.t().contiguous()
         self.gate_up = tuple(gate_up)
         self.down = tuple(down)
         self.top_k = int(top_k)
@@ -109,7 +110,8 @@ class SparseMoeBlock:
         """fp32 router logits [T, E] for tokens x2 [T, H]."""
         if x2.shape[0] <= ROUTER_GEMV_MAX_T:
             return ops.router_logits(x2, self.router_weight, *self.router_quant)
-        return torch.matmul(x2.float(), self._router_f32.t())
+        # bf16 x bf16 products are exact in fp32; fp32 accumulation and output
+        return torch.mm(x2, self._router_dense_t, out_dtype=torch.float32)
 
     def route(self, x2: torch.Tensor):
         """(idx int32 [T, k], scores fp32 [T, k]) for tokens x2 [T, H]."""
