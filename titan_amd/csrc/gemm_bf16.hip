@@ -424,15 +424,12 @@ __device__ __forceinline__ void run_unit(const GemmArgs& a, char* smem, int tile
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  static_assert(kMaxSub == 4, "one tile_loop instance per subtile count 1..kMaxSub");
   switch (msub) {
     case 1: tile_loop<TILED, 1>(c, smem, acc); break;
     case 2: tile_loop<TILED, 2>(c, smem, acc); break;
     case 3: tile_loop<TILED, 3>(c, smem, acc); break;
-    case 4: tile_loop<TILED, 4>(c, smem, acc); break;
-    case 5: tile_loop<TILED, 5>(c, smem, acc); break;
-    case 6: tile_loop<TILED, 6>(c, smem, acc); break;
-    case 7: tile_loop<TILED, 7>(c, smem, acc); break;
-    default: tile_loop<TILED, 8>(c, smem, acc); break;
+    default: tile_loop<TILED, 4>(c, smem, acc); break;
   }
 
   // epilogue: subtile (i, j) holds D^T -- lane l32 is token row 32i + l32,
