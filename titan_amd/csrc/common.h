@@ -48,10 +48,33 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// Sum over groups of W lanes (W a power of two <= 64), result in every lane.
+// v plus lane (l ^ 1), (l ^ 2), mirror-in-8 and rotate-by-8 partners: DPP
+// moves within a 16-lane row, no LDS crossbar (ds_bpermute, which
+// __shfl_xor lowers to, costs a memory round trip per step).
+__device__ __forceinline__ float dpp_add(float v, int ctrl) {
+  switch (ctrl) {  // the control word must be a constant
+    case 0xB1: return v + __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xB1, 0xf, 0xf, false));
+    case 0x4E: return v + __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4E, 0xf, 0xf, false));
+    case 0x141: return v + __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x141, 0xf, 0xf, false));
+    default: return v + __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x128, 0xf, 0xf, false));
+  }
+}
+
+// Sum over aligned groups of W lanes (W a power of two <= 64), result in
+// every lane.  W <= 16 stays inside a DPP row: quad_perm 1,0,3,2 and
+// 2,3,0,1 sum each quad, row_half_mirror pairs the quads of an 8-lane half,
+// row_ror:8 pairs the halves of the row.
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
+  if constexpr (W <= 16) {
+    if constexpr (W >= 2) v = dpp_add(v, 0xB1);   // quad_perm 1,0,3,2
+    if constexpr (W >= 4) v = dpp_add(v, 0x4E);   // quad_perm 2,3,0,1
+    if constexpr (W >= 8) v = dpp_add(v, 0x141);  // row_half_mirror
+    if constexpr (W >= 16) v = dpp_add(v, 0x128); // row_ror:8
+    return v;
+  } else {
 #pragma unroll
-  for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, W);
-  return v;
+    for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, W);
+    return v;
+  }
 }
