@@ -558,3 +558,28 @@ def test_8bit_unsupported_shapes_are_declined(dev):
     with pytest.raises(ops.QmoeUnsupported):
         ops.gate_up_silu(x2, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev),
                          i32_t(np.zeros((1, 2), np.int32), dev), bits=8)
+
+
+@pytest.mark.parametrize("K", [2560, 3584, 5120, 7680])
+def test_decode_gemv_tail_chunk_shapes(dev, orc, K):
+    """K = 2048 n + 512 t: the 2048-chunk GEMV with a partial last chunk
+    (the reference model's hidden size 2560 among them)."""
+    say(f"decode GEMV tail shapes K={K}")
+    rng = np.random.default_rng(K)
+    E, I, k = 16, 256, 4
+    w, s, b = synth.quant_weights(rng, (E, 2 * I), K)
+    x = synth.bf16_bits(rng.normal(size=(2, K)).astype(np.float32))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(2)]).astype(np.int32)
+    h = ops.gate_up_silu(bf16_t(x, dev), words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), i32_t(idx, dev))
+    gu64, _ = orc.gather_qmm_rows(x, np.repeat(np.arange(2), k).astype(np.int32), idx.reshape(-1), w, s, b)
+    h64, _ = orc.swiglu(gu64)
+    assert_close_bf16(orc, bits(h).reshape(2 * k, I), h64, what=f"gate_up K={K}")
+    xr = rng.integers(0, 2, size=9).astype(np.int32)
+    ex = rng.integers(0, E, size=9).astype(np.int32)
+    y = ops.gather_qmv(bf16_t(x, dev), i32_t(xr, dev), i32_t(ex, dev), words_t(w, dev), bf16_t(s, dev),
+                       bf16_t(b, dev))
+    ref64, _ = orc.gather_qmm_rows(x, xr, ex, w, s, b)
+    assert_close_bf16(orc, bits(y), ref64, what=f"gather_qmv K={K}")
+    yq = ops.quantized_matmul(bf16_t(x, dev), words_t(w[0], dev), bf16_t(s[0], dev), bf16_t(b[0], dev))
+    refq, _ = orc.gather_qmm_rows(x, None, np.zeros(2, np.int32), w[:1], s[:1], b[:1])
+    assert_close_bf16(orc, bits(yq), refq, what=f"quantized_matmul K={K}")

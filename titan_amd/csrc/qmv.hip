@@ -311,10 +311,16 @@ __device__ __forceinline__ uint4 load_nt(const uint4* p) {
 // trips (kernel arguments, the expert id, the weights), so the expert id is
 // requested first, x next (it does not wait for the id), then the scales and
 // biases and the codes row by row, in the order they are consumed.
-template <int NV, int MODE, int RG, int GS, bool GATHER, bool XROWS>
+template <int NV, int TL, int MODE, int RG, int GS, bool GATHER, bool XROWS>
 __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
+  // K = 2048 * NV + 512 * TL: NV whole chunks of 64 lanes x 32 elements and,
+  // when TL > 0, a tail chunk held by lanes < 16 * TL (the others load
+  // nothing and contribute zero: x = 0 there)
+  constexpr int NC = NV + (TL > 0 ? 1 : 0);
+  constexpr int KE = 2048 * NV + 512 * TL;
+  static_assert(KE % (8 * GS) == 0, "16-byte scale units per row");
   constexpr int OUTS = MODE == 1 ? RG : 2 * RG;
-  constexpr int G = 2048 * NV / GS;     // groups per row
+  constexpr int G = KE / GS;            // groups per row
   constexpr int UPR = G / 8;            // 16-byte scale units per row
   constexpr int UNITS = 4 * RG * UPR;   // [array][row group][RG rows][UPR]
   constexpr int UPL = (UNITS + 63) / 64;
@@ -326,14 +332,17 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   int e = GATHER ? a.experts[r] : 0;
   const uint32_t xr = XROWS ? (uint32_t)a.x_rows[r] : fast_div(r, a.x_divf);
   const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
-  uint4 xa[NV][4];
+  const bool tail_lane = lane < 16 * TL;  // holds data in the tail chunk
+  uint4 xa[NC][4];
 #pragma unroll
-  for (int v = 0; v < NV; ++v)
+  for (int v = 0; v < NC; ++v)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q];
+    for (int q = 0; q < 4; ++q)
+      xa[v][q] = (v < NV || tail_lane) ? reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q]
+                                       : make_uint4(0u, 0u, 0u, 0u);
 
   e = min(max(e, 0), a.num_experts - 1);
-  constexpr int64_t KW = 2048 * NV / 8;
+  constexpr int64_t KW = KE / 8;
   const int64_t ebase = (int64_t)e * a.n_w;
   const int grp1 = MODE == 1 ? a.n_out + n0 : n0 + RG;
   // row of slot (group g, row i), clamped into the expert (slots past n_out are computed, not stored)
@@ -353,18 +362,19 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
       sbv[j] = *reinterpret_cast<const i32x4_t*>(base + row_of(seg & 1, rem / UPR) * G + (rem % UPR) * 8);
     }
   }
-  uint4 wv[2][RG][NV];
+  uint4 wv[2][RG][NC];
 #pragma unroll
   for (int g = 0; g < 2; ++g)
 #pragma unroll
     for (int i = 0; i < RG; ++i) {
       const uint4* p = reinterpret_cast<const uint4*>(a.w + row_of(g, i) * KW) + lane;
 #pragma unroll
-      for (int v = 0; v < NV; ++v) wv[g][i][v] = load_nt(p + v * 64);
+      for (int v = 0; v < NC; ++v)
+        wv[g][i][v] = (v < NV || tail_lane) ? load_nt(p + v * 64) : make_uint4(0u, 0u, 0u, 0u);
     }
-  XChunk xc[NV];
+  XChunk xc[NC];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
+  for (int v = 0; v < NC; ++v) {
     float s = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -395,8 +405,8 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
     for (int i = 0; i < RG; ++i) {
       float acc = 0.f;
 #pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        const int gi = (v * 2048 + lane * 32) / GS;
+      for (int v = 0; v < NC; ++v) {
+        const int gi = min((v * 2048 + lane * 32) / GS, G - 1);  // tail lanes past K: any group (x = 0)
         const float sv = bf16_to_f32(sbl[((0 * 2 + g) * RG + i) * G + gi]);
         const float bv = bf16_to_f32(sbl[((1 * 2 + g) * RG + i) * G + gi]);
         acc += affine_chunk(dot_chunk(wv[g][i][v], xc[v], mv), xc[v].sum, sv, bv);
@@ -648,26 +658,41 @@ bool pick_split(int64_t K, int* lpr, int* nv) {
   return false;
 }
 
-template <int MODE, int RG, int NV, int GS>
+template <int MODE, int RG, int NV, int TL, int GS>
 int launch_qmv64_k(const QmvArgs& a, dim3 grid, hipStream_t st) {
   if (MODE == 1) {
-    qmv64_kernel<NV, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
   } else if (!a.experts) {
-    qmv64_kernel<NV, MODE, RG, GS, false, false><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, false, false><<<grid, dim3(64), 0, st>>>(a);
   } else if (a.x_rows) {
-    qmv64_kernel<NV, MODE, RG, GS, true, true><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, true, true><<<grid, dim3(64), 0, st>>>(a);
   } else {
-    qmv64_kernel<NV, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
   }
   return qmoe::launch_status("qmv64_kernel");
 }
 
+// K = 2048 * NV + 512 * TL; tails (TL > 0) are instantiated for group 64 only
+template <int MODE, int RG, int NV, int TL>
+int launch_qmv64_tl(const QmvArgs& a, dim3 grid, hipStream_t st) {
+  if constexpr (TL == 0) {
+    switch (a.group_size) {
+      case 32: return launch_qmv64_k<MODE, RG, NV, 0, 32>(a, grid, st);
+      case 64: return launch_qmv64_k<MODE, RG, NV, 0, 64>(a, grid, st);
+      default: return launch_qmv64_k<MODE, RG, NV, 0, 128>(a, grid, st);
+    }
+  } else {
+    return launch_qmv64_k<MODE, RG, NV, TL, 64>(a, grid, st);
+  }
+}
+
 template <int MODE, int RG, int NV>
 int launch_qmv64_nv(const QmvArgs& a, dim3 grid, hipStream_t st) {
-  switch (a.group_size) {
-    case 32: return launch_qmv64_k<MODE, RG, NV, 32>(a, grid, st);
-    case 64: return launch_qmv64_k<MODE, RG, NV, 64>(a, grid, st);
-    default: return launch_qmv64_k<MODE, RG, NV, 128>(a, grid, st);
+  switch ((a.K % 2048) / 512) {
+    case 0: return launch_qmv64_tl<MODE, RG, NV, 0>(a, grid, st);
+    case 1: return launch_qmv64_tl<MODE, RG, NV, 1>(a, grid, st);
+    case 2: return launch_qmv64_tl<MODE, RG, NV, 2>(a, grid, st);
+    default: return launch_qmv64_tl<MODE, RG, NV, 3>(a, grid, st);
   }
 }
 
@@ -681,11 +706,18 @@ int launch_qmv64(const QmvArgs& a, dim3 grid, hipStream_t st) {
   }
 }
 
+// Shapes the 2048-chunk GEMV takes: K = 2048 * n + 512 * t (1 <= n <= 4,
+// t < 4, and t == 0 unless group_size == 64), 4-bit codes.
+bool qmv64_shape(int64_t K, int group_size, int bits) {
+  if (bits != 4 || K < 2048 || K % 512 || K / 2048 > 4) return false;
+  return K % 2048 == 0 || group_size == 64;
+}
+
 template <int MODE>
 int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st, int bits = 4) {
   // qmv64 reads scales and biases 16 bytes at a time: G % 8 == 0 and aligned arrays
   const bool sb_ok = (a.K / a.group_size) % 8 == 0 && qmoe::aligned16(a.s) && qmoe::aligned16(a.b);
-  if (bits == 4 && a.K % 2048 == 0 && a.K / 2048 <= 4 && (sb_ok || lpr == 0)) {
+  if (qmv64_shape(a.K, a.group_size, bits) && (sb_ok || lpr == 0)) {
     if (!sb_ok) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "scales and biases must be 16-byte aligned");
     constexpr int RG = MODE == 1 ? QMOE_QMV_RG_GU : QMOE_QMV_RG_DENSE;
     constexpr int outs = MODE == 1 ? RG : 2 * RG;
@@ -761,8 +793,8 @@ int check_common(int64_t K, int group_size, int bits, int* lpr, int* nv, bool al
   if (group_size != 32 && group_size != 64 && group_size != 128)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "group_size=%d: kernels take 32, 64 or 128", group_size);
   if (K % group_size) return qmoe::fail(QMOE_ERR_INVALID, "K=%lld not a multiple of group_size", (long long)K);
-  // K = 2048*n (n <= 4) always has the qmv64 kernel; other K need a lane split
-  const bool qmv64_ok = bits == 4 && K % 2048 == 0 && K / 2048 <= 4;
+  // K = 2048*n + 512*t (qmv64_shape) always has the qmv64 kernel; other K need a lane split
+  const bool qmv64_ok = qmv64_shape(K, group_size, bits);
   if (!pick_split(K, lpr, nv) && !qmv64_ok)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%lld: needs K = 32*L*n, L in {4,8,16}, n <= 8, or 2048*n, n <= 4",
                       (long long)K);
