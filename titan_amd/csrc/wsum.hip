@@ -2,7 +2,8 @@
 //
 // Each thread owns 8 adjacent columns of one output row and walks the k
 // expert outputs in order, keeping eight partial sums per column (slot j mod 8)
-// that are combined in slot order at the end.  The arithmetic is spelled out
+// that are combined in slot order at the end.  Rows are fetched eight slots
+// at a time, so a thread has eight 16-byte loads in flight.  The arithmetic is spelled out
 // with contraction switched off so no multiply-add is fused: every mode is a
 // fixed sequence of IEEE operations and bf16 roundings, bit-for-bit
 // reproducible against a CPU restatement of the same sequence.
@@ -26,26 +27,34 @@ __global__ __launch_bounds__(256) void wsum_kernel(const uint16_t* __restrict__ 
   for (int a = 0; a < 8; ++a)
 #pragma unroll
     for (int v = 0; v < 8; ++v) acc[a][v] = 0.f;
-  for (int j = 0; j < k; ++j) {
-    const int64_t p = r * k + j;
-    const int64_t src = inv ? (int64_t)inv[p] : p;
-    float s = scores[p];
-    if (MODE >= QMOE_WSUM_OPS) s = round_bf16(s);
-    const uint4 q = *reinterpret_cast<const uint4*>(xs + src * dim + c8);
-    const uint32_t pr[4] = {q.x, q.y, q.z, q.w};
-    const int slot = j & 7;
+  // slots in batches of eight: the batch's indices, scores and rows are all
+  // requested before any is used (eight loads in flight per thread), and
+  // slot j mod 8 is the batch position, a compile-time index
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    uint4 q[8];
+    float sc[8];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const float xv = (v & 1) ? bf16hi(pr[v >> 1]) : bf16lo(pr[v >> 1]);
-      float prod = s * xv;
-      if (kRoundProd) prod = round_bf16(prod);
-      // slot is dynamic; select it with a fully unrolled compare so acc stays in registers
+    for (int jj = 0; jj < 8; ++jj) {
+      if (j0 + jj < k) {
+        const int64_t p = r * k + j0 + jj;
+        const int64_t src = inv ? (int64_t)inv[p] : p;
+        sc[jj] = scores[p];
+        q[jj] = *reinterpret_cast<const uint4*>(xs + src * dim + c8);
+      }
+    }
 #pragma unroll
-      for (int a = 0; a < 8; ++a) {
-        if (a == slot) {
-          float t = acc[a][v] + prod;
-          acc[a][v] = kBfAcc ? round_bf16(t) : t;
-        }
+    for (int jj = 0; jj < 8; ++jj) {
+      if (j0 + jj >= k) break;
+      float s = sc[jj];
+      if (MODE >= QMOE_WSUM_OPS) s = round_bf16(s);
+      const uint32_t pr[4] = {q[jj].x, q[jj].y, q[jj].z, q[jj].w};
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const float xv = (v & 1) ? bf16hi(pr[v >> 1]) : bf16lo(pr[v >> 1]);
+        float prod = s * xv;
+        if (kRoundProd) prod = round_bf16(prod);
+        const float t = acc[jj][v] + prod;
+        acc[jj][v] = kBfAcc ? round_bf16(t) : t;
       }
     }
   }
