@@ -58,9 +58,11 @@ def _route_cases():
     yield "fused-max", rng.integers(0, 512, size=8192).astype(np.int32), 512
     yield "split-min", rng.integers(0, 512, size=8193).astype(np.int32), 512
     yield "zipf-700", synth.make(3, tokens=700)["idx"], 256
+    # more than 2048 experts: the one-wave-per-chunk scatter
+    yield "many-experts", rng.integers(0, 3000, size=9000).astype(np.int32), 3000
 
 
-@pytest.mark.parametrize("case", list(range(8)))
+@pytest.mark.parametrize("case", list(range(9)))
 def test_route_matches_stable_sort(dev, orc, case):
     name, ids, E = list(_route_cases())[case]
     say(f"route {name} n={ids.size} E={E}")

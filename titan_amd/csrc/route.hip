@@ -10,10 +10,12 @@
 //   scan    one block: expert-major exclusive scan of the histograms, which
 //           gives each (expert, chunk) its first output slot, the offsets,
 //           and the tile list
-//   scatter one wave per chunk: walks the chunk in row order 64 rows at a
-//           time; lanes holding the same id find each other with one ballot
-//           per id bit, so a row's slot is its chunk base plus the number of
-//           earlier rows with its id -- a stable sort with no atomics.
+//   scatter four waves per chunk (one for more than 2048 experts), each
+//           walking its quarter in row order 64 rows at a time; lanes
+//           holding the same id find each other with one ballot per id bit,
+//           so a row's slot is its chunk base, plus the rows of its id in the
+//           chunk's earlier quarters, plus the earlier rows of its id in its
+//           own quarter -- a stable sort with no atomics.
 #include "common.h"
 
 namespace {
@@ -43,52 +45,36 @@ __global__ __launch_bounds__(kCountThreads) void route_count_kernel(const int32_
   for (int e = threadIdx.x; e <= E; e += blockDim.x) counts[(int64_t)e * nchunks + blockIdx.x] = hist[e];
 }
 
-// Exclusive scan of one value per thread over the block; also returns the total.
+// Exclusive scan of one value per thread over the block; also returns the
+// total.  Each wave scans its 64 values with shuffles, one wave scans the
+// 16 wave totals, and every thread adds its wave's base: three barriers.
 __device__ int block_exclusive_scan(int v, int* lds, int* total) {
-  const int tid = threadIdx.x;
-  lds[tid] = v;
-  __syncthreads();
-  for (int off = 1; off < kScanThreads; off <<= 1) {
-    const int t = tid >= off ? lds[tid - off] : 0;
-    __syncthreads();
-    lds[tid] += t;
-    __syncthreads();
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  constexpr int kWavesPerBlock = kScanThreads / 64;
+  int x = v;  // inclusive scan within the wave
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
   }
-  *total = lds[kScanThreads - 1];
-  const int incl = lds[tid];
+  if (lane == 63) lds[w] = x;
   __syncthreads();
-  return incl - v;
-}
-
-// Exclusive scan, in place, of a[0..L) with one block.  Each thread owns a
-// contiguous segment, read in batches of 16 independent loads so the reads
-// overlap instead of paying one memory latency per element.
-__device__ int block_scan_array(int32_t* a, int64_t L, int* lds) {
-  const int tid = threadIdx.x;
-  const int64_t seg = (L + kScanThreads - 1) / kScanThreads;
-  const int64_t lo = min((int64_t)tid * seg, L), hi = min(lo + seg, L);
-  int local = 0;
-  for (int64_t b = lo; b < hi; b += 16) {
-    int v[16];
+  if (w == 0) {
+    const int t = lane < kWavesPerBlock ? lds[lane] : 0;
+    int u = t;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = (b + i < hi) ? a[b + i] : 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) local += v[i];
-  }
-  int total;
-  int run = block_exclusive_scan(local, lds, &total);
-  for (int64_t b = lo; b < hi; b += 16) {
-    int v[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = (b + i < hi) ? a[b + i] : 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (b + i < hi) a[b + i] = run;
-      run += v[i];
+    for (int d = 1; d < kWavesPerBlock; d <<= 1) {
+      const int y = __shfl_up(u, d, 64);
+      if (lane >= d) u += y;
     }
+    if (lane < kWavesPerBlock) lds[lane] = u - t;  // exclusive base of wave `lane`
+    if (lane == kWavesPerBlock - 1) lds[kWavesPerBlock] = u;
   }
   __syncthreads();
-  return total;
+  *total = lds[kWavesPerBlock];
+  const int res = lds[w] + x - v;
+  __syncthreads();  // lds is free for the caller's next use
+  return res;
 }
 
 // Tiles from offsets (offsets[0..E] visible to the block): one (row_start,
@@ -119,6 +105,15 @@ __device__ void emit_tiles(const int32_t* offsets, int E, int tile_rows, int32_t
   }
 }
 
+// counts is the [E + 1][nchunks] table of route_count_kernel (row E: ids out
+// of range).  One read pass: each thread keeps its contiguous segment of the
+// table in registers (kSegMax values; a longer table is walked twice),
+// writes back the exclusive prefix over rows 0..E-1 (each (expert, chunk)'s
+// first output slot), reduces row E to the out-of-range count, and hands the
+// expert offsets to the tile emission through LDS.
+constexpr int kSegMax = 16;
+constexpr int kScanMaxE = 8192;
+
 __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int32_t* __restrict__ counts, int64_t n,
                                                                   int E, int nchunks, int tile_rows,
                                                                   int32_t* __restrict__ offsets,
@@ -127,42 +122,92 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int32_t* __res
                                                                   int32_t* __restrict__ ntiles,
                                                                   int64_t max_tiles, int32_t* __restrict__ bad) {
   __shared__ int lds[kScanThreads];
-  // out-of-range count: row E of the histogram table
-  int local = 0;
-  for (int c = threadIdx.x; c < nchunks; c += kScanThreads) local += counts[(int64_t)E * nchunks + c];
+  __shared__ int off[kScanMaxE + 1];
+  const int tid = threadIdx.x;
+  const int64_t Lmain = (int64_t)E * nchunks;
+  const int64_t L = Lmain + nchunks;
+  const int64_t seg = (L + kScanThreads - 1) / kScanThreads;
+  const int64_t lo = min((int64_t)tid * seg, L), hi = min(lo + seg, L);
+  int v[kSegMax];
+  int local = 0, local_bad = 0;
+  if (seg <= kSegMax) {
+#pragma unroll
+    for (int i = 0; i < kSegMax; ++i) v[i] = (lo + i < hi) ? counts[lo + i] : 0;
+#pragma unroll
+    for (int i = 0; i < kSegMax; ++i) {
+      if (lo + i < Lmain) local += v[i];
+      else local_bad += v[i];
+    }
+  } else {
+    for (int64_t i = lo; i < hi; ++i) {
+      if (i < Lmain) local += counts[i];
+      else local_bad += counts[i];
+    }
+  }
   int nbad;
-  block_exclusive_scan(local, lds, &nbad);
-  if (threadIdx.x == 0) bad[0] = nbad;
-  block_scan_array(counts, (int64_t)E * nchunks, lds);
-  for (int e = threadIdx.x; e < E; e += kScanThreads) offsets[e] = nchunks ? counts[(int64_t)e * nchunks] : 0;
-  if (threadIdx.x == 0) offsets[E] = (int32_t)n;
+  block_exclusive_scan(local_bad, lds, &nbad);
+  if (tid == 0) bad[0] = nbad;
+  int total;
+  int run = block_exclusive_scan(local, lds, &total);
+  // an expert's offset is the prefix at its chunk-0 entry, index e * nchunks
+  if (seg <= kSegMax) {
+#pragma unroll
+    for (int i = 0; i < kSegMax; ++i) {
+      const int64_t idx = lo + i;
+      if (idx < hi && idx < Lmain) {
+        counts[idx] = run;
+        if (idx % nchunks == 0) off[idx / nchunks] = run;
+        run += v[i];
+      }
+    }
+  } else {
+    for (int64_t idx = lo; idx < hi && idx < Lmain; ++idx) {
+      const int c = counts[idx];
+      counts[idx] = run;
+      if (idx % nchunks == 0) off[idx / nchunks] = run;
+      run += c;
+    }
+  }
+  if (nchunks == 0)
+    for (int e = tid; e < E; e += kScanThreads) off[e] = 0;  // no rows: every segment is empty
+  if (tid == 0) off[E] = (int)n;
   __syncthreads();
-  emit_tiles(offsets, E, tile_rows, tile_row, tile_exp, ntiles, max_tiles, lds);
+  for (int e = tid; e <= E; e += kScanThreads) offsets[e] = off[e];
+  emit_tiles(off, E, tile_rows, tile_row, tile_exp, ntiles, max_tiles, lds);
 }
 
-__global__ __launch_bounds__(64) void route_scatter_kernel(const int32_t* __restrict__ ids, int64_t n, int E,
-                                                           int nbits, int nchunks,
-                                                           const int32_t* __restrict__ base,
-                                                           int32_t* __restrict__ order,
-                                                           int32_t* __restrict__ inv_order,
-                                                           int32_t* __restrict__ sorted_ids) {
-  extern __shared__ int run[];  // E
-  const int lane = threadIdx.x;
+// Stable scatter of one 1024-row chunk by W waves, wave w taking rows
+// w * 1024/W .. in order.  Pass 1 matches equal ids within each 64-row step
+// (one ballot per id bit), keeps the match masks and counts the wave's rows
+// per id in its LDS row; a prefix over the waves, per id, turns the counts
+// into each wave's first slot (the chunk's base from the scan first); pass 2
+// ranks each row among the earlier rows of its id and writes it.
+template <int W>
+__global__ __launch_bounds__(64 * W) void route_scatter_kernel(const int32_t* __restrict__ ids, int64_t n, int E,
+                                                               int nbits, int nchunks,
+                                                               const int32_t* __restrict__ base,
+                                                               int32_t* __restrict__ order,
+                                                               int32_t* __restrict__ inv_order,
+                                                               int32_t* __restrict__ sorted_ids) {
+  extern __shared__ int run[];  // [W][E]
+  constexpr int kSteps = kChunk / 64 / W;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = blockIdx.x;
-  for (int e = lane; e < E; e += 64) run[e] = base[(int64_t)e * nchunks + c];
-  __syncthreads();
+  int* my = run + w * E;
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  constexpr int kSteps = kChunk / 64;
-  int idv[kSteps];  // the chunk's ids, loaded up front (independent loads)
+  const int64_t r0 = (int64_t)c * kChunk + (int64_t)w * (kChunk / W);
+  int idv[kSteps];  // the wave's ids, loaded up front (independent loads)
 #pragma unroll
   for (int step = 0; step < kSteps; ++step) {
-    const int64_t i = (int64_t)c * kChunk + step * 64 + lane;
+    const int64_t i = r0 + step * 64 + lane;
     idv[step] = i < n ? clamp_id(ids[i], E) : E;  // E: sentinel, never written
   }
+  for (int e = threadIdx.x; e < W * E; e += 64 * W) run[e] = 0;
+  __syncthreads();
+  uint64_t mv[kSteps];
 #pragma unroll
   for (int step = 0; step < kSteps; ++step) {
-    const int64_t i = (int64_t)c * kChunk + step * 64 + lane;
-    const bool valid = i < n;
+    const bool valid = r0 + step * 64 + lane < n;
     const int id = idv[step];
     uint64_t m = __ballot(valid);
     if (!valid) m = ~m;
@@ -171,16 +216,37 @@ __global__ __launch_bounds__(64) void route_scatter_kernel(const int32_t* __rest
       const uint64_t bb = __ballot(bit);
       m &= bit ? bb : ~bb;
     }
+    mv[step] = m;
+    if (valid && __popcll(m & lt) == 0) my[id] += __popcll(m);  // one leader per id and step
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 64 * W) {
+    int b = base[(int64_t)e * nchunks + c];
+#pragma unroll
+    for (int q = 0; q < W; ++q) {
+      const int t = run[q * E + e];
+      run[q * E + e] = b;
+      b += t;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int step = 0; step < kSteps; ++step) {
+    const int64_t i = r0 + step * 64 + lane;
+    const bool valid = i < n;
+    const int id = idv[step];
+    const uint64_t m = mv[step];
     const int rank = __popcll(m & lt);
     if (valid) {
-      const int dst = run[id] + rank;
+      const int dst = my[id] + rank;
       order[dst] = (int32_t)i;
       sorted_ids[dst] = id;
       inv_order[i] = dst;
     }
-    __syncthreads();
-    if (valid && rank == 0) run[id] += __popcll(m);
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();  // every lane has read my[id] before the leader moves it
+    if (valid && rank == 0) my[id] += __popcll(m);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -367,8 +433,12 @@ extern "C" int qmoe_route(const int32_t* ids, int64_t n_pairs, int32_t num_exper
   if (rc || nch == 0) return rc;
   int nbits = 1;
   while ((1 << nbits) <= num_experts) ++nbits;  // ids in [0, E] (E is the sentinel)
-  route_scatter_kernel<<<dim3((unsigned)nch), dim3(64), num_experts * sizeof(int), st>>>(
-      ids, n_pairs, num_experts, nbits, (int)nch, counts, order, inv_order, sorted_ids);
+  if (num_experts <= 2048)  // four waves per chunk: 4 * E ints of LDS
+    route_scatter_kernel<4><<<dim3((unsigned)nch), dim3(256), 4 * num_experts * sizeof(int), st>>>(
+        ids, n_pairs, num_experts, nbits, (int)nch, counts, order, inv_order, sorted_ids);
+  else
+    route_scatter_kernel<1><<<dim3((unsigned)nch), dim3(64), num_experts * sizeof(int), st>>>(
+        ids, n_pairs, num_experts, nbits, (int)nch, counts, order, inv_order, sorted_ids);
   return qmoe::launch_status("route_scatter_kernel");
 }
 
