@@ -13,7 +13,7 @@ is timed with events on the stream it is replayed on.  The other four
 workloads are measured the same way and reported under ``configs``; the CPU
 baseline is the oracle's C restatement timed on this host.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--configs 0,1,2,3,4]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--configs 0,1,2,3,4,5,6,7]
 """
 
 from __future__ import annotations
@@ -217,51 +217,42 @@ def traffic_from_profile():
     return None
 
 
-def _rounds_for(k, most=8):
-    """The largest divisor of k that is at most `most`."""
-    return max(r for r in range(1, min(most, k) + 1) if k % r == 0)
-
-
-def time_graph(fn_list, warmup, dev):
-    """Split the K launches of fn_list into R <= 8 consecutive chunks, capture
-    each chunk as a graph, run `warmup` eager steps and one untimed replay of
-    every chunk, then time one replay of each chunk with events on the replay
-    stream.  Exactly K steps are timed; consecutive chunks use different
-    weight sets.  Returns (median seconds per step, {"min", "median", "rounds"})."""
+def time_graph(fn_list, warmup, dev, extra_rounds=4):
+    """Capture the K launches of fn_list as one graph, run `warmup` eager steps
+    and one untimed replay, then time one replay -- exactly K steps -- with
+    events on the replay stream.  `extra_rounds` further replays give the min
+    and median per step as a spread indicator; the returned seconds per step
+    come from the first timed replay.  Returns (seconds per step,
+    {"min", "median", "rounds", "graphs"})."""
     import statistics
 
     import torch
 
     k = len(fn_list)
-    r = _rounds_for(k)
-    n = k // r
     for i in range(warmup):
         fn_list[i % k]()
     torch.cuda.synchronize()
-    graphs = []
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
-    for c in range(r):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(s):
-            with torch.cuda.graph(g, stream=s):
-                for fn in fn_list[c * n:(c + 1) * n]:
-                    fn()
-        graphs.append(g)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for fn in fn_list:
+                fn()
     torch.cuda.synchronize()
-    for g in graphs:
-        g.replay()
+    g.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(r + 1)]
-    ev[0].record(st)
-    for c, g in enumerate(graphs):
+    per = []
+    for _ in range(1 + extra_rounds):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(st)
         g.replay()
-        ev[c + 1].record(st)
-    torch.cuda.synchronize()
-    per = [ev[c].elapsed_time(ev[c + 1]) / 1e3 / n for c in range(r)]
-    med = statistics.median(per)
-    return med, {"min": min(per), "median": med, "rounds": r, "graphs": graphs}
+        e1.record(st)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / 1e3 / k)
+    return per[0], {"min": min(per), "median": statistics.median(per), "rounds": len(per), "graphs": [g]}
 
 
 # --------------------------------------------------------------- workloads

@@ -56,24 +56,31 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restri
 
 // ---------------------------------------------------------------- GEMM
 //
-// Work unit: one (128-row tile, 256-column block); a block's eight waves
-// (two per SIMD) own 32 columns each and all the tile's rows.  Persistent
-// blocks, one per CU, take units heavy-first (gemm_common.h).  Per 64-wide K group g every
-// operand byte reaches LDS through asynchronous copies into a ring of three
-// stages:
+// Work unit: one (128-row tile, 256-column block).  A block has sixteen waves,
+// four per SIMD at no more than 128 VGPRs each: wave w owns the 32 columns of
+// column group cw = w % 8 and the 16-row subtiles of parity rh = w / 8 (rh,
+// rh + 2, ...), so both parities have rows on a short tile.  Persistent
+// blocks, one per CU, take units heavy-first (gemm_common.h).  Per 64-wide K
+// group g every operand byte reaches LDS through asynchronous copies into a
+// ring of kStages stages:
 //   A  the tile's int8 activation rows, 128 x 64 bytes, gathered through
-//      x_rows, 16-byte unit u of row r stored at u ^ aswz(r);
-//   B  each wave's 32 columns of packed codes (tile layout: half a 2 KiB
-//      chunk; MLX layout: 16 bytes per lane from the column's row);
-//   S  the columns' scales and biases.
-// A wave turns its code words into int8 with byte permutes (codes 0..15 are
-// valid int8: no zero point), runs one v_mfma_i32_16x16x64_i8 per 16 x 16
-// subtile and group (D_g exact in int32) and folds acc += s * D_g in fp32;
-// wave w < the tile's 16-row subtile count also takes subtile w's exact row
-// sums R_g with v_dot4 and keeps them in LDS as int16 (|R_g| <= 64 * 127).
-// After the last group the bias term sum_g b[n,g] R_g[m] is a small bf16 MFMA
-// product per subtile (R split into exact bf16 hi + lo), the rows are scaled
-// by sx and the tile leaves through LDS as 512-byte row segments.
+//      x_rows, 16-byte unit u of row r stored at u ^ aswz(r); the parity-1
+//      wave of column group cw copies rows 16cw .. +15;
+//   B  column group cw's packed codes (tile layout: half a 2 KiB chunk; MLX
+//      layout: 16 bytes per lane from the column's row), copied by its
+//      parity-0 wave;
+//   S  the scales of the 64-column block holding those columns (with the
+//      biases in the tile layout's scale|bias words), copied by the same
+//      wave; the bias term reads the biases once per tile, after the loop.
+// After the barrier that publishes group g, a wave turns its code words into
+// int8 with byte permutes (codes 0..15 are valid int8: no zero point), runs
+// one v_mfma_i32_16x16x64_i8 per 16 x 16 subtile (D_g exact in int32) and
+// folds acc += s * D_g in fp32; the parity-1 wave of column group cw also
+// takes subtile cw's exact row sums R_g with v_dot4 and keeps them in LDS as
+// int16 (|R_g| <= 64 * 127).  After the last group the bias term
+// sum_g b[n,g] R_g[m] is a small bf16 MFMA product per subtile (R split into
+// exact bf16 hi + lo), the rows are scaled by sx and the tile leaves through
+// LDS as 512-byte row segments.
 //
 // K order inside a group is free as long as both operands agree: lane
 // quarter qq of the 16 x 16 x 64 MFMA supplies group elements 16qq .. +15 of
@@ -82,11 +89,18 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restri
 using namespace qmoe_gemm;
 
 constexpr int kBM = kTileRows;  // 128
-constexpr int kWaves = 8;        // two per SIMD: one wave's rescale fills the other's waits
+constexpr int kWaves = 16;       // four per SIMD: the others' rescale fills one wave's waits
 constexpr int kCols = 32;        // columns per wave
-constexpr int kBN = kCols * kWaves;
+constexpr int kColGroups = 8;    // column groups per block; two waves (row parities) each
+constexpr int kBN = kCols * kColGroups;
 constexpr int kI8Threads = 64 * kWaves;
-constexpr int kStages = 3;
+// Ring depth: the copies of group g + kStages - 1 go out during group g, so
+// kStages - 2 groups of copies stay in flight past the one waited for.
+#ifndef QMOE_I8_STAGES
+#define QMOE_I8_STAGES 3
+#endif
+constexpr int kStages = QMOE_I8_STAGES;
+static_assert(kStages >= 3, "the ring needs a stage being read, one landing and one in flight");
 constexpr int kMaxG = 64;  // K <= 4096
 constexpr int kI8BlocksPerCU = 1;
 // Row sums R_g[row] live in LDS as int16 [group][kRStride]: consecutive rows
@@ -94,25 +108,27 @@ constexpr int kI8BlocksPerCU = 1;
 // pad shifts successive groups by one bank.
 constexpr int kRStride = kTileRows + 2;
 
-// Stage layout: A rows; B one 1 KiB code copy per wave (its 32 columns);
-// S the scale|bias words (tile layout) or scale and bias pairs (MLX layout)
-// of the 64-column block holding the wave's columns, one 256-byte copy each.
+// Stage layout: A rows; B one 1 KiB code copy per column group (its 32
+// columns); S the scale|bias words (tile layout) or the scale pairs of two
+// consecutive groups (MLX layout) of the 64-column block holding the group's
+// columns, one 256-byte copy each.
 template <bool TILED>
 struct ICfg {
   static constexpr int kAOff = 0;
   static constexpr int kABytes = kBM * 64;
   static constexpr int kBOff = kAOff + kABytes;
-  static constexpr int kBBytes = kWaves * 1024;
+  static constexpr int kBBytes = kColGroups * 1024;
   static constexpr int kSOff = kBOff + kBBytes;
-  static constexpr int kSBytes = kWaves * (TILED ? 1 : 2) * 64 * 4;
+  static constexpr int kSBytes = kColGroups * 64 * 4;
   static constexpr int kStageBytes = kSOff + kSBytes;
   static constexpr int kRingBytes = kStages * kStageBytes;
   static constexpr int kRBytes = kRStride * kMaxG * 2;  // int16 row sums [group][row]
   static constexpr int kLdsBytes = kRingBytes + kRBytes + kBM * 4;  // + sx of the tile's rows
   static_assert(kI8BlocksPerCU * (kLdsBytes + 4 * kMaxOrder) <= 160 * 1024, "LDS per CU");
   static_assert(kRingBytes >= 64 * 512, "the epilogue stages 64 rows of 512 bytes in the ring");
-  static constexpr int kACopies = kABytes / (kWaves * 1024);  // 1 KiB copies per wave
-  static constexpr int kCopies = kACopies + 1 + (TILED ? 1 : 2);
+  static_assert(kABytes == kColGroups * 1024, "one 1 KiB activation copy per parity-1 wave");
+  static constexpr int kCopies0 = 2;  // a parity-0 wave's copies per group: B and S
+  static constexpr int kCopies1 = 1;  // a parity-1 wave's: A
 };
 
 struct Int8Args {
@@ -136,13 +152,12 @@ struct Int8Args {
 
 template <bool TILED>
 struct ICtx {
-  const char* a_src[ICfg<TILED>::kACopies];  // activation 16-byte unit of the lane's row, group 0
-  const char* b_src;
+  const char* a_src;  // parity 1: the lane's activation 16-byte unit, group 0
+  const char* b_src;  // parity 0: codes and scales of group 0
   const char* s_src;
-  const char* z_src;
   uint32_t lds;
   int G;
-  int wave, lane, l32, h;
+  int rh, cw, lane;  // row parity and column group: wave-uniform
 };
 
 // 16 codes (two words, k order 0..15) -> 16 int8 in natural k order.
@@ -157,57 +172,52 @@ __device__ __forceinline__ i32x4_t codes_to_i8(uint32_t wa, uint32_t wb) {
   return r;
 }
 
+// This wave's copies of group g into its ring stage.
 template <bool TILED>
-__device__ __forceinline__ void issue_copy(const ICtx<TILED>& c, int g, int d) {
+__device__ __forceinline__ void issue_group(const ICtx<TILED>& c, int g) {
   using C = ICfg<TILED>;
   const uint32_t st = c.lds + (uint32_t)(g % kStages) * C::kStageBytes;
-  if (d < C::kACopies) {
-    dma16(c.a_src[d] + (size_t)g * 64, st + C::kAOff + (uint32_t)(d * kWaves + c.wave) * 1024);
+  if (c.rh) {
+    dma16(c.a_src + (size_t)g * 64, st + C::kAOff + (uint32_t)c.cw * 1024);
     return;
   }
-  const int j = d - C::kACopies;
   if constexpr (TILED) {
-    if (j == 0) dma16(c.b_src + (size_t)g * 2048, st + C::kBOff + (uint32_t)c.wave * 1024);
-    else dma4(c.s_src + (size_t)g * 256, st + C::kSOff + c.wave * 256);
+    dma16(c.b_src + (size_t)g * 2048, st + C::kBOff + (uint32_t)c.cw * 1024);
+    dma4(c.s_src + (size_t)g * 256, st + C::kSOff + c.cw * 256);
   } else {
-    if (j == 0) dma16(c.b_src + (size_t)g * 32, st + C::kBOff + (uint32_t)c.wave * 1024);
-    else if (j == 1) dma4(c.s_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.wave * 512);
-    else dma4(c.z_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.wave * 512 + 256);
+    dma16(c.b_src + (size_t)g * 32, st + C::kBOff + (uint32_t)c.cw * 1024);
+    dma4(c.s_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.cw * 256);
   }
 }
 
+// Wait until this wave's copies of the oldest group still in flight have
+// landed (the kStages - 2 newer groups may stay outstanding).
 template <bool TILED>
-__device__ __forceinline__ void issue_group(const ICtx<TILED>& c, int g) {
-#pragma unroll
-  for (int d = 0; d < ICfg<TILED>::kCopies; ++d) issue_copy<TILED>(c, g, d);
+__device__ __forceinline__ void wait_oldest(const ICtx<TILED>& c) {
+  if (c.rh) wait_vmem<(kStages - 2) * ICfg<TILED>::kCopies1>();
+  else wait_vmem<(kStages - 2) * ICfg<TILED>::kCopies0>();
 }
 
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
-// Accumulators of a wave: its 32 columns as two 16-column subtiles jj and
-// the tile's rows as up to eight 16-row subtiles i; D[m][n] of a 16 x 16
+// Accumulators of a wave: its 32 columns as two 16-column subtiles jj and its
+// up to four 16-row subtiles j (tile subtile 2j + rh); D[m][n] of a 16 x 16
 // MFMA tile sits in lane n (mod 16), register r at row 4 * (lane / 16) + r.
 constexpr int kJJ = kCols / 16;
-typedef f32x4_t Acc[2 * kMaxSub][kJJ];
+typedef f32x4_t Acc[kMaxSub][kJJ];
 
 // Row swizzle of the 16-byte units of a 64-byte activation row in LDS: unit
-// u of row r is stored at u ^ aswz(r).  Conflict-free for 16-byte reads of
-// one unit by consecutive rows whether the LDS serves 8 lanes per pass over
-// 32 banks (aswz takes distinct values on each parity among r .. r+7) or 16
-// lanes over 64 banks (distinct on each residue mod 4 among r .. r+15).
-__device__ __forceinline__ int aswz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
+// u of row r is stored at u ^ aswz(r).  A 16-byte read by a 16 x 16 x 64
+// fragment has lane quarter qq read unit qq of rows r0 .. r0 + 15.  gfx950
+// serves such a read 32 consecutive lanes (two quarters, 512 bytes) at a
+// time, so rows r and r + 8, whose units share bank positions, must use
+// different unit pairs: aswz(r + 8) = aswz(r) ^ 3.  Within rows 0..7 the
+// units of equal row parity differ, which also keeps 8- and 16-lane passes
+// conflict-free.  aswz(16 i + l) = aswz(l).
+__device__ __forceinline__ int aswz(int row) { return ((row >> 1) & 3) ^ (3 * ((row >> 3) & 1)); }
 
-// Main loop over the groups of one tile with MSUB 32-row subtiles.  Per group
-// and 16 x 16 subtile one v_mfma_i32_16x16x64_i8 covers the whole group;
-// lane quarter qq supplies group elements 16qq .. +15 of its row (A: unit qq
-// of the activation row) and of its column (B: code words 2(qq%2), +1 of the
-// chunk lane (qq/2, column % 32)).  The MFMAs of row subtile i + 1 are issued
-// before subtile i is rescaled, so the matrix core and the vector unit
-// overlap; the copies of group g + 2 go out between subtiles.
-// The wave's weight-side operands of one group: int8 code fragments and the
-// scales of its two 16-column subtiles.  Every wave copies its own code and
-// scale chunk, so it may read them as soon as its own copies have landed,
-// before the barrier that publishes the activation rows copied by all waves.
+// The weight-side operands of one group: int8 code fragments and the scales
+// of the wave's two 16-column subtiles.
 struct BState {
   i32x4_t bq[kJJ];
   float sc[kJJ];
@@ -220,48 +230,47 @@ __device__ __forceinline__ BState load_bstate(const ICtx<TILED>& c, const char* 
   BState b;
 #pragma unroll
   for (int jj = 0; jj < kJJ; ++jj) {
-    const int cc = 16 * jj + l16;  // column within the wave's 32
-    const uint2 wd = *reinterpret_cast<const uint2*>(st + C::kBOff + c.wave * 1024 + ((qq >> 1) * 32 + cc) * 16 +
+    const int cc = 16 * jj + l16;  // column within the group's 32
+    const uint2 wd = *reinterpret_cast<const uint2*>(st + C::kBOff + c.cw * 1024 + ((qq >> 1) * 32 + cc) * 16 +
                                                      (qq & 1) * 8);
     b.bq[jj] = codes_to_i8(wd.x, wd.y);
-    const int sc_i = 32 * (c.wave & 1) + cc;  // the column within its 64-column block
+    const int sc_i = 32 * (c.cw & 1) + cc;  // the column within its 64-column block
     if constexpr (TILED) {
-      const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.wave * 256);
+      const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.cw * 256);
       b.sc[jj] = __uint_as_float(sw[sc_i] << 16);
     } else {
-      const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.wave * 512);
+      const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.cw * 256);
       b.sc[jj] = __uint_as_float((sw[sc_i] << ((g & 1) ? 0 : 16)) & 0xFFFF0000u);
     }
   }
   return b;
 }
 
-// Main loop over the groups of one tile with MSUB 32-row subtiles.  Per group
-// and 16 x 16 subtile one v_mfma_i32_16x16x64_i8 covers the whole group;
-// lane quarter qq supplies group elements 16qq .. +15 of its row (A: unit qq
-// of the activation row) and of its column (B: code words 2(qq%2), +1 of the
-// chunk lane (qq/2, column % 32)).  The MFMAs of row subtile i + 1 are issued
-// before subtile i is rescaled, so the matrix core and the vector unit
-// overlap; the copies of group g + 2 go out between subtiles, and the next
-// group's code fragments and scales are read at the end of the iteration.
+// Main loop over the groups of one tile whose rows fill MSUB 32-row subtiles:
+// the wave has MSUB 16-row subtiles (tile subtiles 2j + rh).  Per group and
+// 16 x 16 subtile one v_mfma_i32_16x16x64_i8 covers the whole group; lane
+// quarter qq supplies group elements 16qq .. +15 of its row (A: unit qq of the
+// activation row) and of its column (B: code words 2(qq%2), +1 of the chunk
+// lane (qq/2, column % 32)).  The MFMAs of subtile j + 1 are issued before
+// subtile j is rescaled, so the matrix core and the vector unit overlap; the
+// copies of group g + kStages - 1 go out after the first subtile's MFMAs.
 template <bool TILED, int MSUB>
 __device__ __forceinline__ void tile_loop_i8(const ICtx<TILED>& c, char* smem, Acc& acc) {
   using C = ICfg<TILED>;
-  constexpr int D = C::kCopies;
-  constexpr int NI = 2 * MSUB;  // 16-row subtiles
   const int G = c.G;
   const int l16 = c.lane & 15, qq = c.lane >> 4;
-  const int aoff = l16 * 64 + ((qq ^ aswz(l16)) * 16);  // the lane's A unit in row subtile 0
+  const int unit_off = l16 * 64 + ((qq ^ aswz(l16)) * 16);  // the lane's A unit within a subtile
+  const int aoff = 16 * c.rh * 64 + unit_off;                // ... within the wave's first subtile
   int16_t* rsum = reinterpret_cast<int16_t*>(smem + C::kRingBytes);
-  issue_group<TILED>(c, 0);
-  issue_group<TILED>(c, min(1, G - 1));
-  wait_vmem<D>();  // this wave's copies of group 0
-  BState bs = load_bstate<TILED>(c, smem, 0);
+#pragma unroll
+  for (int p = 0; p < kStages - 1; ++p) issue_group<TILED>(c, min(p, G - 1));
+  wait_oldest<TILED>(c);  // this wave's copies of group 0
   for (int g = 0; g < G; ++g) {
-    // every wave's copies of group g have landed
+    // every wave's copies of group g have landed, and every wave is done with
+    // the stage that group g + kStages - 1 overwrites
     __builtin_amdgcn_s_barrier();
-    const int cg = min(g + 2, G - 1);
     const char* st = smem + (g % kStages) * C::kStageBytes;
+    const BState bs = load_bstate<TILED>(c, st, g);
     const char* abuf = st + C::kAOff + aoff;
     i32x4_t dc[kJJ], dn[kJJ];
     {
@@ -272,10 +281,11 @@ __device__ __forceinline__ void tile_loop_i8(const ICtx<TILED>& c, char* smem, A
         dc[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bs.bq[jj], z, 0, 0, 0);
       }
     }
+    issue_group<TILED>(c, min(g + kStages - 1, G - 1));
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      if (i + 1 < NI) {
-        const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf + (i + 1) * 16 * 64);
+    for (int j = 0; j < MSUB; ++j) {
+      if (j + 1 < MSUB) {
+        const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf + (j + 1) * 32 * 64);
 #pragma unroll
         for (int jj = 0; jj < kJJ; ++jj) {
           const i32x4_t z = {};
@@ -283,34 +293,28 @@ __device__ __forceinline__ void tile_loop_i8(const ICtx<TILED>& c, char* smem, A
         }
       }
 #pragma unroll
-      for (int q = 0; q < D; ++q)
-        if (q * NI / D == i) issue_copy<TILED>(c, cg, q);
-#pragma unroll
       for (int jj = 0; jj < kJJ; ++jj) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][jj][r] = __builtin_fmaf(bs.sc[jj], (float)dc[jj][r], acc[i][jj][r]);
+        for (int r = 0; r < 4; ++r) acc[j][jj][r] = __builtin_fmaf(bs.sc[jj], (float)dc[jj][r], acc[j][jj][r]);
         // keep the rescale here, between this subtile's and the next one's
         // MFMAs, rather than sunk to the end of the group
-        asm volatile("" : "+v"(acc[i][jj]));
+        asm volatile("" : "+v"(acc[j][jj]));
       }
 #pragma unroll
       for (int jj = 0; jj < kJJ; ++jj) dc[jj] = dn[jj];
     }
-    // exact row sums of the group: wave w takes 16-row subtile w (16 int8 per
-    // lane, four lane quarters per row)
-    if (c.wave < NI) {
-      const int i = c.wave;
-      const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf + i * 16 * 64);
+    // exact row sums of the group: the parity-1 wave of column group cw takes
+    // tile subtile cw (16 int8 per lane, four lane quarters per row)
+    if (c.rh && c.cw < 2 * MSUB) {
+      const i32x4_t af = *reinterpret_cast<const i32x4_t*>(st + C::kAOff + c.cw * 16 * 64 + unit_off);
       int part = 0;
 #pragma unroll
       for (int t = 0; t < 4; ++t) part = __builtin_amdgcn_sdot4(af[t], 0x01010101, part, false);
       part += __shfl_xor(part, 16, 64);
       part += __shfl_xor(part, 32, 64);
-      if (qq == 0) rsum[g * kRStride + 16 * i + l16] = (int16_t)part;
+      if (qq == 0) rsum[g * kRStride + 16 * c.cw + l16] = (int16_t)part;
     }
-    // this wave's copies of group g + 1 (group g + 2's may be in flight)
-    wait_vmem<D>();
-    if (g + 1 < G) bs = load_bstate<TILED>(c, smem + ((g + 1) % kStages) * C::kStageBytes, g + 1);
+    wait_oldest<TILED>(c);  // this wave's copies of group g + 1
   }
   wait_vmem<0>();  // the trailing repeat copies
 }
@@ -325,7 +329,7 @@ __device__ __forceinline__ void finish_tile(const Int8Args& a, char* smem, const
   const int l16 = c.lane & 15, qq = c.lane >> 4;
   const int16_t* rsum = reinterpret_cast<const int16_t*>(smem + C::kRingBytes);
   const float* sxl = reinterpret_cast<const float*>(smem + C::kRingBytes + C::kRBytes);
-  const int col0 = nblk * kBN + c.wave * kCols;
+  const int col0 = nblk * kBN + c.cw * kCols;
   for (int g0 = 0; g0 < G; g0 += 32) {
     // lane quarter qq supplies groups g0 + 8qq .. +7
     i32x4_t bz[kJJ];
@@ -351,8 +355,9 @@ __device__ __forceinline__ void finish_tile(const Int8Args& a, char* smem, const
                        (int)(v[6] | (v[7] << 16))};
     }
 #pragma unroll
-    for (int i = 0; i < 2 * kMaxSub; ++i) {
-      if (i >= 2 * msub) break;
+    for (int j = 0; j < kMaxSub; ++j) {
+      if (j >= msub) break;
+      const int i = 2 * j + c.rh;  // tile subtile
       uint32_t hi[4], lo[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -370,35 +375,51 @@ __device__ __forceinline__ void finish_tile(const Int8Args& a, char* smem, const
       const i32x4_t al = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
 #pragma unroll
       for (int jj = 0; jj < kJJ; ++jj) {
-        acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ah),
-                                                             __builtin_bit_cast(bf16x8_t, bz[jj]), acc[i][jj], 0, 0, 0);
-        acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, al),
-                                                             __builtin_bit_cast(bf16x8_t, bz[jj]), acc[i][jj], 0, 0, 0);
+        acc[j][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ah),
+                                                             __builtin_bit_cast(bf16x8_t, bz[jj]), acc[j][jj], 0, 0, 0);
+        acc[j][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, al),
+                                                             __builtin_bit_cast(bf16x8_t, bz[jj]), acc[j][jj], 0, 0, 0);
       }
     }
   }
-  // out = sx * acc through LDS, 64 rows per pass; staging row m holds the
-  // block's 256 columns (512 bytes), 16-byte unit u at u ^ (m & 31).
+  // out = sx * acc through LDS, 64 rows (tile subtiles 4p .. 4p + 3) per
+  // pass.  Lane (qq, 4a + k) holds column 4a + k of rows 4qq .. 4qq + 3 of a
+  // 16 x 16 subtile; two quad-lane exchanges give it row 4qq + k of columns
+  // 4a .. 4a + 3 as two bf16 pairs, one 8-byte granule.  Staging row m holds
+  // the block's 256 columns (512 bytes), granule gi at gi ^ 4 (m & 7), so the
+  // granule writes of 32 lanes (8 rows x 4 granules) and the 16-byte row
+  // reads below (unit u at u ^ 2 (m & 7)) are conflict-free.
   char* ep = smem;
   const int tid = threadIdx.x;
+  const int k = c.lane & 3, a4 = l16 >> 2;
+  // stage-1 byte selectors: lane parity 0 keeps its low halves, 1 its high
+  const uint32_t sel1 = (k & 1) ? 0x03020706u : 0x05040100u;
+  const bool hiq = (k & 2) != 0;
   uint16_t* obase = a.out + row0 * (int64_t)a.N + nblk * kBN;
   for (int p = 0; 2 * p < msub; ++p) {
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 2 * kMaxSub; ++i) {
-      if ((i >> 2) != p) continue;
+    for (int j = 0; j < kMaxSub; ++j) {
+      if ((j >> 1) != p) continue;  // tile subtile 2j + rh lies in rows 64p .. 64p + 63
+      const int i = 2 * j + c.rh;
+      const float4 sc4 = *reinterpret_cast<const float4*>(sxl + 16 * i + 4 * qq);  // rows 16i + 4qq .. +3
+      const int m = 16 * i + 4 * qq + k - 64 * p;  // the lane's row within the pass after the exchange
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int mt = 16 * i + 4 * qq + r;  // row within the tile
-        const int m = mt - 64 * p;           // row within the pass
-        const float scale = sxl[mt];
-#pragma unroll
-        for (int jj = 0; jj < kJJ; ++jj) {
-          const int col = c.wave * kCols + 16 * jj + l16;  // column within the block
-          const int u = col >> 3;
-          *reinterpret_cast<uint16_t*>(ep + m * 512 + ((u ^ (m & 31)) * 16) + (col & 7) * 2) =
-              (uint16_t)(cvt_pk_bf16(scale * acc[i][jj][r], 0.f) & 0xFFFFu);
-        }
+      for (int jj = 0; jj < kJJ; ++jj) {
+        // own column: rows (0, 1) and (2, 3) as bf16 pairs
+        const uint32_t p0 = cvt_pk_bf16(sc4.x * acc[j][jj][0], sc4.y * acc[j][jj][1]);
+        const uint32_t p1 = cvt_pk_bf16(sc4.z * acc[j][jj][2], sc4.w * acc[j][jj][3]);
+        // with lane k ^ 1: rows 2t + (k & 1) of columns (k & 2, (k & 2) + 1)
+        const uint32_t q0 = __builtin_amdgcn_update_dpp(0u, p0, 0xB1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
+        const uint32_t q1 = __builtin_amdgcn_update_dpp(0u, p1, 0xB1, 0xf, 0xf, false);
+        const uint32_t a0 = __builtin_amdgcn_perm(q0, p0, sel1);
+        const uint32_t a1 = __builtin_amdgcn_perm(q1, p1, sel1);
+        // with lane k ^ 2: row k of column pairs 0 and 1
+        const uint32_t keep = hiq ? a1 : a0;
+        const uint32_t recv = __builtin_amdgcn_update_dpp(0u, hiq ? a0 : a1, 0x4E, 0xf, 0xf, false);  // 2,3,0,1
+        const int gi = c.cw * 8 + 4 * jj + a4;  // granule of columns 4a .. 4a + 3 within the block's row
+        *reinterpret_cast<uint2*>(ep + m * 512 + ((gi ^ (4 * (m & 7))) * 8)) =
+            hiq ? make_uint2(recv, keep) : make_uint2(keep, recv);
       }
     }
     __syncthreads();
@@ -407,7 +428,7 @@ __device__ __forceinline__ void finish_tile(const Int8Args& a, char* smem, const
       const int m = it * (kI8Threads / 32) + tid / 32;
       const int u = tid % 32;
       const int row = 64 * p + m;
-      const uint4 v = *reinterpret_cast<const uint4*>(ep + m * 512 + ((u ^ (m & 31)) * 16));
+      const uint4 v = *reinterpret_cast<const uint4*>(ep + m * 512 + ((u ^ (2 * (m & 7))) * 16));
       if (row < valid) *reinterpret_cast<uint4*>(obase + (int64_t)row * a.N + u * 8) = v;
     }
   }
@@ -427,46 +448,45 @@ __device__ __forceinline__ void run_unit_i8(const Int8Args& a, char* smem, int t
 
   ICtx<TILED> c;
   c.G = G;
-  c.wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  c.rh = wave / kColGroups;
+  c.cw = wave % kColGroups;
   c.lane = tid % 64;
-  c.l32 = c.lane % 32;
-  c.h = c.lane / 32;
   c.lds = (uint32_t)(uintptr_t)smem;
-  // A copy q of wave w writes stage bytes (4q + w) * 1024 + lane * 16: row
-  // 16(4q + w) + lane/4, stored unit lane%4 holding logical unit
-  // (lane%4) ^ aswz(row).  Rows past the tile repeat its last row.
+  c.a_src = c.b_src = c.s_src = nullptr;
   float* sxl = reinterpret_cast<float*>(smem + C::kRingBytes + C::kRBytes);
-#pragma unroll
-  for (int q = 0; q < C::kACopies; ++q) {
-    const int row = 16 * (q * kWaves + c.wave) + (c.lane >> 2);
+  if (c.rh) {
+    // The copy writes stage bytes cw * 1024 + lane * 16: row 16 cw + lane / 4,
+    // stored unit lane % 4 holding logical unit (lane % 4) ^ aswz(row).  Rows
+    // past the tile repeat its last row.
+    const int row = 16 * c.cw + (c.lane >> 2);
     const int unit = (c.lane & 3) ^ aswz(row);
     int64_t src = row0 + min(row, valid - 1);
     if (a.x_rows) src = a.x_rows[src];
-    c.a_src[q] = reinterpret_cast<const char*>(a.xi + src * K + unit * 16);
+    c.a_src = reinterpret_cast<const char*>(a.xi + src * K + unit * 16);
+  } else {
+    // the group's 32 columns: half (cw & 1) of the 64-column block nblk * 4 + cw / 2
+    const int c64 = nblk * (kBN / 64) + c.cw / 2;
+    if constexpr (TILED) {
+      const int64_t chunk0 = ((int64_t)e * (a.N / 64) + c64) * G;
+      c.b_src = reinterpret_cast<const char*>(a.w) + (chunk0 * 2 + (c.cw & 1)) * 1024 + c.lane * 16;
+      c.s_src = reinterpret_cast<const char*>(a.sb) + chunk0 * 256 + c.lane * 4;
+    } else {
+      const int64_t KW = K / 8;
+      const int64_t col64 = (int64_t)e * a.N + c64 * 64;
+      c.b_src = reinterpret_cast<const char*>(a.w + (col64 + 32 * (c.cw & 1) + c.lane % 32) * KW + (c.lane / 32) * 4);
+      c.s_src = reinterpret_cast<const char*>(a.s + (col64 + c.lane) * G);
+    }
   }
   if (tid < kBM) {
     int64_t src = row0 + min(tid, valid - 1);
     if (a.x_rows) src = a.x_rows[src];
     sxl[tid] = a.sx[src];
   }
-  // the wave's 32 columns: half (wave & 1) of the 64-column block nblk * 4 + wave / 2
-  const int c64 = nblk * (kBN / 64) + c.wave / 2;
-  if constexpr (TILED) {
-    const int64_t chunk0 = ((int64_t)e * (a.N / 64) + c64) * G;
-    c.b_src = reinterpret_cast<const char*>(a.w) + (chunk0 * 2 + (c.wave & 1)) * 1024 + c.lane * 16;
-    c.s_src = reinterpret_cast<const char*>(a.sb) + chunk0 * 256 + c.lane * 4;
-    c.z_src = nullptr;
-  } else {
-    const int64_t KW = K / 8;
-    const int64_t col64 = (int64_t)e * a.N + c64 * 64;
-    c.b_src = reinterpret_cast<const char*>(a.w + (col64 + 32 * (c.wave & 1) + c.l32) * KW + c.h * 4);
-    c.s_src = reinterpret_cast<const char*>(a.s + (col64 + c.lane) * G);
-    c.z_src = reinterpret_cast<const char*>(a.b + (col64 + c.lane) * G);
-  }
 
   Acc acc;
 #pragma unroll
-  for (int i = 0; i < 2 * kMaxSub; ++i)
+  for (int i = 0; i < kMaxSub; ++i)
 #pragma unroll
     for (int j = 0; j < kJJ; ++j)
 #pragma unroll
@@ -478,12 +498,14 @@ __device__ __forceinline__ void run_unit_i8(const Int8Args& a, char* smem, int t
     case 3: tile_loop_i8<TILED, 3>(c, smem, acc); break;
     default: tile_loop_i8<TILED, 4>(c, smem, acc); break;
   }
+  static_assert(kMaxSub == 4, "tile_loop_i8 is instantiated for 1..4 subtiles per parity");
   __syncthreads();  // row sums and sx visible to every wave; the ring is free
   finish_tile<TILED>(a, smem, c, acc, e, row0, valid, msub, nblk);
 }
 
+// The second bound is the minimum number of waves per SIMD.
 template <bool TILED>
-__global__ __launch_bounds__(kI8Threads, kI8BlocksPerCU) void gemm_int8_kernel(Int8Args a) {
+__global__ __launch_bounds__(kI8Threads, kI8BlocksPerCU * kWaves / 4) void gemm_int8_kernel(Int8Args a) {
   using C = ICfg<TILED>;
   __shared__ __attribute__((aligned(1024))) char smem[C::kLdsBytes];
   __shared__ int order[kMaxOrder];
