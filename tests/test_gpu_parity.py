@@ -399,6 +399,10 @@ def test_sorted_gemm_int8_every_subtile_count(dev, orc):
     rxi, rsx = orc.quant_act_int8(x)
     ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, None, ids, w, s, b)
     assert_close_bf16(orc, bits(y), ref64, what="int8 gemm every subtile count")
+    # the MLX-layout kernel takes the same rows to the same bits
+    ym = ops.gather_qmm_int8_sorted(xi, sx, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), tiles)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(ym), bits(y))
 
 
 def test_sorted_gemm_int8_cfg4_sampled(dev, orc):

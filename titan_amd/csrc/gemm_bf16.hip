@@ -290,32 +290,44 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, char* smem, const 
                                            int nblk) {
   constexpr int kPassRows = 64;
   char* ep = smem;  // the ring is free once every wave has left the main loop
-  const int tid = threadIdx.x;
-  uint16_t* obase = a.out + row0 * (int64_t)a.N + nblk * kBN;
+  // the thread index through an empty asm: the epilogue's lane offsets are
+  // then computed here, not hoisted out of the unit loop and spilled across
+  // the main loop (a spill reload waits for every store still in flight)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int l32 = tid % 32, h = (tid % 64) / 32;
+  uint16_t* obase = a.out + uniform64(row0 * (int64_t)a.N + nblk * kBN);
   for (int p = 0; 2 * p < msub; ++p) {
     __syncthreads();  // the ring (first pass) or the previous pass's rows are no longer read
 #pragma unroll
     for (int i = 0; i < kMaxSub; ++i) {
       if ((i >> 1) != p) continue;
-      const int m = 32 * (i & 1) + c.l32;  // row within the pass; m & 31 == l32
+      const int m = 32 * (i & 1) + l32;  // row within the pass; m & 31 == l32
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int gi = (c.wave * 64 + 32 * j + 8 * q + 4 * c.h) / 4;  // 8-byte granule within the row
+          const int gi = (c.wave * 64 + 32 * j + 8 * q + 4 * h) / 4;  // 8-byte granule within the row
           const uint2 v = make_uint2(cvt_pk_bf16(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
                                      cvt_pk_bf16(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
-          *reinterpret_cast<uint2*>(ep + m * 512 + (gi ^ (2 * c.l32)) * 8) = v;
+          *reinterpret_cast<uint2*>(ep + m * 512 + (gi ^ (2 * l32)) * 8) = v;
         }
     }
     __syncthreads();
+    constexpr int kIt = kPassRows * 32 / kThreads;
+    i32x4_t v[kIt];
 #pragma unroll
-    for (int it = 0; it < kPassRows * 32 / kThreads; ++it) {
+    for (int it = 0; it < kIt; ++it) {
       const int m = it * (kThreads / 32) + tid / 32;
-      const int u = tid % 32;
+      lds_read16(v[it], ep + m * 512 + (((tid % 32) ^ (m & 31)) * 16));
+    }
+    lds_wait_all(v);
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int m = it * (kThreads / 32) + tid / 32;
       const int row = kPassRows * p + m;
-      const uint4 v = *reinterpret_cast<const uint4*>(ep + m * 512 + ((u ^ (m & 31)) * 16));
-      if (row < valid) *reinterpret_cast<uint4*>(obase + (int64_t)row * a.N + u * 8) = v;
+      // block-uniform base + 32-bit offset: SGPR-based stores, no 64-bit row pointers
+      if (row < valid) *reinterpret_cast<i32x4_t*>(obase + (uint32_t)(row * a.N + (tid % 32) * 8)) = v[it];
     }
   }
 }
@@ -335,14 +347,19 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, char* smem,
   constexpr int kHBlock = kBN / 2;  // h columns per block
   const int NH = a.N / 2;
   char* ep = smem;
-  const int tid = threadIdx.x;
+  // the thread index through an empty asm: the epilogue's lane offsets are
+  // then computed here, not hoisted out of the unit loop and spilled across
+  // the main loop (a spill reload waits for every store still in flight)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int l32 = tid % 32, h = (tid % 64) / 32;
   uint16_t* obase = a.out + row0 * (int64_t)NH + nblk * kHBlock;
   for (int p = 0; 2 * p < msub; ++p) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kMaxSub; ++i) {
       if ((i >> 1) != p) continue;
-      const int m = 32 * (i & 1) + c.l32;  // row within the pass
+      const int m = 32 * (i & 1) + l32;  // row within the pass
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float hv[4];
@@ -351,19 +368,25 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, char* smem,
           const float g = acc[i][0][4 * q + t], u = acc[i][1][4 * q + t];
           hv[t] = g / (1.0f + __expf(-g)) * u;
         }
-        const int gi = (c.wave * 32 + 8 * q + 4 * c.h) / 4;  // 8-byte granule within the 256-byte row
+        const int gi = (c.wave * 32 + 8 * q + 4 * h) / 4;  // 8-byte granule within the 256-byte row
         const uint2 v = make_uint2(cvt_pk_bf16(hv[0], hv[1]), cvt_pk_bf16(hv[2], hv[3]));
         *reinterpret_cast<uint2*>(ep + m * 256 + ((((gi >> 1) ^ (m & 15)) << 1) | (gi & 1)) * 8) = v;
       }
     }
     __syncthreads();
+    constexpr int kIt = kPassRows * 16 / kThreads;
+    i32x4_t v[kIt];
 #pragma unroll
-    for (int it = 0; it < kPassRows * 16 / kThreads; ++it) {
+    for (int it = 0; it < kIt; ++it) {
       const int m = it * (kThreads / 16) + tid / 16;
-      const int u = tid % 16;
+      lds_read16(v[it], ep + m * 256 + (((tid % 16) ^ (m & 15)) * 16));
+    }
+    lds_wait_all(v);
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int m = it * (kThreads / 16) + tid / 16;
       const int row = kPassRows * p + m;
-      const uint4 v = *reinterpret_cast<const uint4*>(ep + m * 256 + ((u ^ (m & 15)) * 16));
-      if (row < valid) *reinterpret_cast<uint4*>(obase + (int64_t)row * NH + u * 8) = v;
+      if (row < valid) *reinterpret_cast<i32x4_t*>(obase + (uint32_t)(row * NH + (tid % 16) * 8)) = v[it];
     }
   }
 }

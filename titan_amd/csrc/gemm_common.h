@@ -45,6 +45,31 @@ __device__ __forceinline__ void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// A 64-bit value every lane holds alike, moved to scalar registers, so that
+// stores address base + 32-bit lane offset (SGPR base) and keep no 64-bit
+// per-lane pointers live.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// 16-byte LDS reads whose results are only waited for together: an epilogue
+// reads all of a pass's staged row pieces, then stores them.  (Written as
+// plain loads, the compiler sinks each read next to its row-guarded store,
+// and every read's latency is exposed.)  The reads are asm, so the compiler
+// does not track them: lds_wait_all waits for them and passes the values on
+// through empty asm, which keeps every use after the wait.
+__device__ __forceinline__ void lds_read16(i32x4_t& v, const void* p) {
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"((uint32_t)(uintptr_t)p));
+}
+template <int N>
+__device__ __forceinline__ void lds_wait_all(i32x4_t (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
 
 // Two floats -> packed bf16 pair (low half = a), round to nearest even.
