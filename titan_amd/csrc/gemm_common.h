@@ -61,7 +61,7 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
 // does not track them: lds_wait_all waits for them and passes the values on
 // through empty asm, which keeps every use after the wait.
 __device__ __forceinline__ void lds_read16(i32x4_t& v, const void* p) {
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"((uint32_t)(uintptr_t)p));
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"((uint32_t)(uintptr_t)p) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void lds_wait_all(i32x4_t (&v)[N]) {
