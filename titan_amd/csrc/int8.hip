@@ -123,7 +123,12 @@ struct ICfg {
   static constexpr int kStageBytes = kSOff + kSBytes;
   static constexpr int kRingBytes = kStages * kStageBytes;
   static constexpr int kRBytes = kRStride * kMaxG * 2;  // int16 row sums [group][row]
-  static constexpr int kLdsBytes = kRingBytes + kRBytes + kBM * 4;  // + sx of the tile's rows
+  static constexpr int kSxOff = kRingBytes + kRBytes;  // sx of the tile's rows
+  // tile layout: the bias halves of the scale|bias words, saved as the groups
+  // stream past, bf16 [column group][group][32 columns], for the bias term
+  static constexpr int kBiasOff = kSxOff + kBM * 4;
+  static constexpr int kBiasBytes = TILED ? kColGroups * kMaxG * 32 * 2 : 0;
+  static constexpr int kLdsBytes = kBiasOff + kBiasBytes;
   static_assert(kI8BlocksPerCU * (kLdsBytes + 4 * kMaxOrder) <= 160 * 1024, "LDS per CU");
   static_assert(kRingBytes >= 64 * 512, "the epilogue stages 64 rows of 512 bytes in the ring");
   static_assert(kABytes == kColGroups * 1024, "one 1 KiB activation copy per parity-1 wave");
@@ -221,6 +226,7 @@ __device__ __forceinline__ int aswz(int row) { return ((row >> 1) & 3) ^ (3 * ((
 struct BState {
   i32x4_t bq[kJJ];
   float sc[kJJ];
+  uint32_t bias[kJJ];  // tile layout: the columns' bias bits (bf16)
 };
 
 template <bool TILED>
@@ -238,6 +244,7 @@ __device__ __forceinline__ BState load_bstate(const ICtx<TILED>& c, const char* 
     if constexpr (TILED) {
       const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.cw * 256);
       b.sc[jj] = __uint_as_float(sw[sc_i] << 16);
+      b.bias[jj] = sw[sc_i] >> 16;
     } else {
       const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.cw * 256);
       b.sc[jj] = __uint_as_float((sw[sc_i] << ((g & 1) ? 0 : 16)) & 0xFFFF0000u);
@@ -271,6 +278,14 @@ __device__ __forceinline__ void tile_loop_i8(const ICtx<TILED>& c, char* smem, A
     __builtin_amdgcn_s_barrier();
     const char* st = smem + (g % kStages) * C::kStageBytes;
     const BState bs = load_bstate<TILED>(c, st, g);
+    if constexpr (TILED) {
+      // the parity-0 wave keeps its columns' biases of group g for the bias term
+      if (!c.rh && qq == 0) {
+        uint16_t* bl = reinterpret_cast<uint16_t*>(smem + C::kBiasOff) + (c.cw * kMaxG + g) * 32;
+#pragma unroll
+        for (int jj = 0; jj < kJJ; ++jj) bl[16 * jj + l16] = (uint16_t)bs.bias[jj];
+      }
+    }
     const char* abuf = st + C::kAOff + aoff;
     i32x4_t dc[kJJ], dn[kJJ];
     {
@@ -343,8 +358,7 @@ __device__ __forceinline__ void finish_tile(const Int8Args& a, char* smem, const
         uint32_t bits = 0;
         if (g < G) {
           if constexpr (TILED) {
-            const int64_t chunk = ((int64_t)e * (a.N / 64) + n / 64) * G + g;
-            bits = a.sb[chunk * 64 + (n & 63)] >> 16;
+            bits = reinterpret_cast<const uint16_t*>(smem + C::kBiasOff)[(c.cw * kMaxG + g) * 32 + (n - col0)];
           } else {
             bits = a.b[((int64_t)e * a.N + n) * G + g];
           }
