@@ -248,6 +248,7 @@ __device__ __forceinline__ BState load_bstate(const ICtx<TILED>& c, const char* 
     } else {
       const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.cw * 256);
       b.sc[jj] = __uint_as_float((sw[sc_i] << ((g & 1) ? 0 : 16)) & 0xFFFF0000u);
+      b.bias[jj] = 0u;  // the MLX layout's biases are read by the bias term itself
     }
   }
   return b;
