@@ -130,8 +130,8 @@ static int cmp_pair(const void* a, const void* b) {
 }
 
 /* Rows grouped by expert so each expert's weights are dequantised once;
- * semantics are per row (Appendix of the survey: mx.gather_qmm with
- * transpose=True, switch_layers.py:87-98, moe_gather_ws.py:403-414). */
+ * semantics are per row (mx.gather_qmm with transpose=True:
+ * switch_layers.py:87-98, moe_gather_ws.py:403-414). */
 void orc_gather_qmm_rows(const uint16_t* x, int64_t K, const int32_t* x_rows,
                          const int32_t* experts, int64_t n_rows,
                          const uint32_t* w, const uint16_t* s, const uint16_t* b,
