@@ -20,6 +20,25 @@ namespace {
 // ---------------------------------------------------------------- quantizer
 
 // One wave per row; each lane owns K/64 consecutive elements (a multiple of 8).
+// Rows up to K = 4096 (64 elements per lane) stay in registers between the
+// max pass and the quantising pass; longer rows are read again.
+constexpr int kQuantRegElems = 64;
+
+// 8 bf16 of one 16-byte load -> 8 int8, rint(x / sc) clamped to [-127, 127]
+// (sc == 0: zeros), packed low byte first.
+__device__ __forceinline__ uint2 quant_pack(const uint4 q, float sc) {
+  const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+  uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float xv = (j & 1) ? bf16hi(v[j >> 1]) : bf16lo(v[j >> 1]);
+    float t = sc == 0.f ? 0.f : rintf(__fdiv_rn(xv, sc));
+    t = fminf(fmaxf(t, -127.f), 127.f);
+    packed[j >> 2] |= ((uint32_t)(int)t & 0xFFu) << (8 * (j & 3));
+  }
+  return make_uint2(packed[0], packed[1]);
+}
+
 __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restrict__ x, int64_t R, int K,
                                                         int8_t* __restrict__ xi, float* __restrict__ sx) {
   const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
@@ -27,30 +46,36 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restri
   if (r >= R) return;
   const int per = K / 64;
   const uint16_t* xr = x + r * K + lane * per;
-  float amax = 0.f;
-  for (int i = 0; i < per; i += 8) {
-    const uint4 q = *reinterpret_cast<const uint4*>(xr + i);
+  int8_t* out = xi + r * K + lane * per;
+  auto absmax8 = [](float m, const uint4 q) {
     const uint32_t v[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fmaxf(fabsf(bf16lo(v[j])), fabsf(bf16hi(v[j]))));
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf16lo(v[j])), fabsf(bf16hi(v[j]))));
+    return m;
+  };
+  uint4 kept[kQuantRegElems / 8];
+  float amax = 0.f;
+  if (per <= kQuantRegElems) {  // wave-uniform: static register indices, all loads in flight together
+#pragma unroll
+    for (int t = 0; t < kQuantRegElems / 8; ++t)
+      if (8 * t < per) kept[t] = *reinterpret_cast<const uint4*>(xr + 8 * t);
+#pragma unroll
+    for (int t = 0; t < kQuantRegElems / 8; ++t)
+      if (8 * t < per) amax = absmax8(amax, kept[t]);
+  } else {
+    for (int i = 0; i < per; i += 8) amax = absmax8(amax, *reinterpret_cast<const uint4*>(xr + i));
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
   const float sc = __fdiv_rn(amax, 127.0f);
   if (lane == 0) sx[r] = sc;
-  int8_t* out = xi + r * K + lane * per;
-  for (int i = 0; i < per; i += 8) {
-    const uint4 q = *reinterpret_cast<const uint4*>(xr + i);
-    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
-    uint32_t packed[2] = {0u, 0u};
+  if (per <= kQuantRegElems) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float xv = (j & 1) ? bf16hi(v[j >> 1]) : bf16lo(v[j >> 1]);
-      float t = sc == 0.f ? 0.f : rintf(__fdiv_rn(xv, sc));
-      t = fminf(fmaxf(t, -127.f), 127.f);
-      packed[j >> 2] |= ((uint32_t)(int)t & 0xFFu) << (8 * (j & 3));
-    }
-    *reinterpret_cast<uint2*>(out + i) = make_uint2(packed[0], packed[1]);
+    for (int t = 0; t < kQuantRegElems / 8; ++t)
+      if (8 * t < per) *reinterpret_cast<uint2*>(out + 8 * t) = quant_pack(kept[t], sc);
+  } else {
+    for (int i = 0; i < per; i += 8)
+      *reinterpret_cast<uint2*>(out + i) = quant_pack(*reinterpret_cast<const uint4*>(xr + i), sc);
   }
 }
 
