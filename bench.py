@@ -50,6 +50,7 @@ def parse():
     ap.add_argument("--only", default=None,
                     help="run one workload's timed loop only, or 'copy' for the calibration copy kernel")
     ap.add_argument("--eager", action="store_true", help="launch the timed steps eagerly (no graph)")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak probes")
     ap.add_argument("--traffic", action="store_true",
                     help="measure the decode kernel's HBM traffic live with rocprofv3 counter passes")
     return ap.parse_args()
@@ -98,28 +99,24 @@ def weight_sets(wl, n_sets, dev, seed):
     return sets
 
 
-def n_sets_for(wl, rotate_gb):
-    per = wl["w"].nbytes + wl["s"].nbytes + wl["b"].nbytes
-    return max(1, int(np.ceil(rotate_gb * 1e9 / per)))
-
-
-def time_eager(fn_list, warmup, dev):
-    """Eager launches (used under counter collection)."""
+def time_eager(cycle, steps, warmup, dev):
+    """The first `steps` launches of the cycle, eagerly (used under counter
+    collection, where each dispatch is profiled on its own)."""
     import torch
 
     for i in range(warmup):
-        fn_list[i % len(fn_list)]()
+        cycle[i % len(cycle)]()
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     st = torch.cuda.current_stream()
     e0.record(st)
-    for fn in fn_list:
+    for fn in cycle[:steps]:
         fn()
     e1.record(st)
     torch.cuda.synchronize()
-    sec = e0.elapsed_time(e1) / 1e3 / len(fn_list)
-    return sec, {"min": sec, "median": sec, "rounds": 1, "graphs": None}
+    sec = e0.elapsed_time(e1) / 1e3 / steps
+    return sec, {"min": sec, "median": sec, "max": sec, "rounds": 1, "windows": 1, "graphs": None}
 
 
 CALIBRATION_MIB = 256
@@ -217,70 +214,169 @@ def traffic_from_profile():
     return None
 
 
-def time_graph(fn_list, warmup, dev, extra_rounds=4):
-    """Capture the K launches of fn_list as one graph, run `warmup` eager steps
-    and ~0.3 s of untimed replays, then time one replay -- exactly K steps --
-    with events on the replay stream, enqueued right behind the untimed ones.
-    `extra_rounds` further replays give the min and median per step as a
-    spread indicator; the returned seconds per step come from the first timed
-    replay.  Returns (seconds per step, {"min", "median", "rounds", "graphs"})."""
+def cycle_len(steps: int, per_call_bytes: float, rotate_bytes: float) -> int:
+    """Launches in one rotation cycle: at least `steps` and enough that the
+    cycle touches `rotate_bytes` of distinct weights, rounded up to whole
+    windows of exactly `steps` launches."""
+    need = max(steps, int(np.ceil(rotate_bytes / max(per_call_bytes, 1.0))))
+    return steps * int(np.ceil(need / steps))
+
+
+def time_graph(cycle, steps, warmup, dev, min_rounds=7):
+    """Time a rotation cycle of launches in windows of exactly `steps`.
+
+    The cycle (a multiple of `steps` long) is cut into windows of `steps`
+    consecutive launches, each captured as one graph.  After `warmup` eager
+    launches and ~0.3 s of untimed replays of the whole cycle, max(min_rounds,
+    windows) windows are replayed back to back in cycle order, each bracketed by
+    events on the replay stream (no host sync in between: the GPU never waits
+    for the host to submit a graph).  Consecutive windows continue the cycle, so
+    a weight byte comes back only after the whole cycle's other bytes have
+    streamed past.  Returns (median seconds per step, {"min", "median", "max",
+    "rounds", "windows", "graphs"})."""
     import statistics
 
     import torch
 
-    k = len(fn_list)
+    L = len(cycle)
+    assert L % steps == 0, (L, steps)
     for i in range(warmup):
-        fn_list[i % k]()
+        cycle[i % L]()
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
-    g = torch.cuda.CUDAGraph()
+    graphs = []
     with torch.cuda.stream(s):
-        with torch.cuda.graph(g, stream=s):
-            for fn in fn_list:
-                fn()
+        for w in range(L // steps):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for fn in cycle[w * steps:(w + 1) * steps]:
+                    fn()
+            graphs.append(g)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    g.replay()
+    for g in graphs:
+        g.replay()
     torch.cuda.synchronize()
     n_warm = min(50, max(1, int(0.3 / max(time.perf_counter() - t0, 1e-4))))
-    # ~0.3 s of untimed replays (the first replays after capture run slower:
-    # clocks ramp under sustained load), then the timed replays, all enqueued
-    # back to back: no host sync in between, so the GPU never waits for the
-    # host to submit a graph's launches
     st = torch.cuda.current_stream()
     for _ in range(n_warm):
-        g.replay()
+        for g in graphs:
+            g.replay()
+    rounds = max(min_rounds, len(graphs))
     evs = []
-    for _ in range(1 + extra_rounds):
+    for r in range(rounds):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(st)
-        g.replay()
+        graphs[r % len(graphs)].replay()
         e1.record(st)
         evs.append((e0, e1))
     torch.cuda.synchronize()
-    per = [e0.elapsed_time(e1) / 1e3 / k for e0, e1 in evs]
-    return per[0], {"min": min(per), "median": statistics.median(per), "rounds": len(per), "graphs": [g]}
+    per = [e0.elapsed_time(e1) / 1e3 / steps for e0, e1 in evs]
+    med = statistics.median(per)
+    return med, {"min": min(per), "median": med, "max": max(per), "rounds": rounds, "windows": len(graphs),
+                 "graphs": graphs}
+
+
+def timer(args):
+    return time_eager if args.eager else time_graph
+
+
+# ------------------------------------------------------------ measured peaks
+
+
+def measure_peaks(dev, read_gib=4):
+    """What this part sustains, with the probe kernels of libqmoe_peaks.so: a
+    streaming read of `read_gib` GiB (beyond the 256 MB Infinity Cache) and
+    dense bf16 / int8 MFMA loops over random register operands.  Medians of
+    five timed runs after one warm-up."""
+    import ctypes
+    import statistics
+
+    import torch
+    from titan_amd import build as tbuild
+
+    L = ctypes.CDLL(str(tbuild.PEAKS_LIB))
+    for name in ("qmoe_peak_stream_read", "qmoe_peak_mfma_bf16", "qmoe_peak_mfma_i8"):
+        getattr(L, name).restype = ctypes.c_int
+    L.qmoe_peak_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    L.qmoe_peak_mfma_bf16.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    L.qmoe_peak_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    nbytes = read_gib * 2 ** 30
+    buf = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).random_()
+    sink = torch.zeros(max(L.qmoe_peak_stream_blocks(), L.qmoe_peak_mfma_waves()), dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream()
+
+    def timed(launch, reps=5):
+        launch()
+        torch.cuda.synchronize()
+        out = []
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            launch()
+            e1.record(st)
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1) / 1e3)
+        return statistics.median(out)
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(f"peak probe failed (code {rc})")
+
+    t_read = timed(lambda: check(L.qmoe_peak_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), st.cuda_stream)))
+    iters = 20000
+    waves = L.qmoe_peak_mfma_waves()
+    t_bf16 = timed(lambda: check(L.qmoe_peak_mfma_bf16(iters, sink.data_ptr(), st.cuda_stream)))
+    t_i8 = timed(lambda: check(L.qmoe_peak_mfma_i8(iters, sink.data_ptr(), st.cuda_stream)))
+    del buf
+    torch.cuda.empty_cache()
+    return {"hbm_read_GBps": round(nbytes / t_read / 1e9, 1),
+            "bf16_mfma_TFLOPs": round(waves * iters * 4 * 32768 / t_bf16 / 1e12, 1),
+            "int8_mfma_TOPs": round(waves * iters * 4 * 65536 / t_i8 / 1e12, 1),
+            "method": f"stream read of {read_gib} GiB (16-byte non-temporal loads, 2048 blocks); "
+                      f"{waves} waves x {iters} x 4 independent v_mfma_f32_32x32x16_bf16 / "
+                      "v_mfma_i32_32x32x32_i8 on random register operands; median of 5"}
 
 
 # --------------------------------------------------------------- workloads
+#
+# Every setup returns (workload, cycle, meta): `cycle` is the rotation of
+# launches timed in windows of exactly --steps (time_graph), long enough that
+# its weight bytes exceed --rotate-gb, with weight sets sized so that a cycle
+# touches every weight byte at most about once.
+
+
+MAX_ROTATION_BYTES = 16e9  # cap on the weight sets one workload keeps resident
+
+
+def n_sets_needed(wl, cycle_bytes, rotate_gb):
+    per = wl["w"].nbytes + wl["s"].nbytes + wl["b"].nbytes
+    want = min(max(rotate_gb * 1e9, cycle_bytes), MAX_ROTATION_BYTES)
+    return max(1, int(np.ceil(want / per)))
 
 
 def setup_cfg1(args, dev):
-    """Decode gate_up + SwiGLU: 10 experts of one token."""
+    """Decode gate_up + SwiGLU: 10 experts of one token.  Each launch reads 10
+    experts no other launch of the cycle reads (sets x 256 experts, dealt out
+    by per-set permutations)."""
     import torch
     from titan_amd import ops, synth
 
     wl = synth.make(1)
-    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 101)
+    per_call = synth.algorithmic_bytes(1)
+    L = cycle_len(args.steps, per_call, args.rotate_gb * 1e9)
+    sets = weight_sets(wl, max(n_sets_needed(wl, L * per_call, args.rotate_gb), int(np.ceil(L * 10 / 256))), dev,
+                       101)
     rng = np.random.default_rng(1001)
     x = to_dev(wl["x"], "bf16", dev)
     E = wl.meta["E"]
     perms = [rng.permutation(E) for _ in sets]
     cursor = [0] * len(sets)
     idxs = []
-    for i in range(args.steps):
+    for i in range(L):
         si = i % len(sets)
         if cursor[si] + 10 > E:
             perms[si] = rng.permutation(E)
@@ -313,20 +409,24 @@ def setup_cfg1(args, dev):
                           torch.cuda.current_stream().cuda_stream)
         return f
 
-    return wl, [mk_mlx(i) for i in range(args.steps)], {
-        "bytes": synth.algorithmic_bytes(1), "flops": synth.algorithmic_flops(1), "bound": "hbm",
+    return wl, [mk_mlx(i) for i in range(L)], {
+        "bytes": per_call, "flops": synth.algorithmic_flops(1), "bound": "hbm",
         "kernel": "qmv64_kernel<1, 0, 1, 4, 64, true, false>", "sets": len(sets),
-        "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(args.steps)]),
+        "cycle_bytes": L * per_call,
+        "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(L)]),
         "workload": "decode gate_up gather_qmm + SwiGLU: 1 token, H=2048, E=256, top_k=10, "
                     "W [256,1024,2048] int4 g64 bf16 scale/bias -> h [10,512]"}
 
 
 def setup_cfg0(args, dev):
+    """Dense quantized_matmul: every launch of the cycle reads its own weight set."""
     import torch
     from titan_amd import ops, synth
 
     wl = synth.make(0)
-    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 100)
+    per_call = synth.algorithmic_bytes(0)
+    L = cycle_len(args.steps, per_call, args.rotate_gb * 1e9)
+    sets = weight_sets(wl, min(L, n_sets_needed(wl, L * per_call, args.rotate_gb)), dev, 100)
     x = to_dev(wl["x"], "bf16", dev)
     out = torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)
     tsets = [ops.repack_tiles(w[None], s[None], b[None]) for (w, s, b) in sets]
@@ -348,29 +448,32 @@ def setup_cfg0(args, dev):
                           b.data_ptr(), 4096, 64, 4, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
         return f
 
-    return wl, [mk_mlx(i) for i in range(args.steps)], {
-        "bytes": synth.algorithmic_bytes(0), "flops": synth.algorithmic_flops(0), "bound": "hbm",
+    return wl, [mk_mlx(i) for i in range(L)], {
+        "bytes": per_call, "flops": synth.algorithmic_flops(0), "bound": "hbm",
         "kernel": "qmv64_kernel<1, 0, 0, 2, 64, false, false>", "sets": len(sets),
-        "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(args.steps)]),
+        "cycle_bytes": min(L, len(sets)) * per_call,
+        "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(L)]),
         "workload": "dense quantized_matmul x [1,2048] . W [4096,2048] int4 g64"}
 
 
 def setup_cfg2(args, dev):
+    """Decode down + weighted sum, 8 tokens: a fresh routing per launch (the
+    workload's distinct-expert statistics), weight sets cycled."""
     import torch
     from titan_amd import ops, synth
 
     wl = synth.make(2)
-    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 102)
+    est_call = wl.meta["distinct"] * 2048 * (256 + 32)
+    L = cycle_len(args.steps, est_call, args.rotate_gb * 1e9)
+    sets = weight_sets(wl, n_sets_needed(wl, L * est_call, args.rotate_gb), dev, 102)
     h = to_dev(wl["h"], "bf16", dev)
     idx = to_dev(wl["idx"], "i32", dev)
     sc = to_dev(wl["scores"], "f32", dev)
     rng = np.random.default_rng(1002)
-    # per step: a fresh routing (same distinct-expert statistics), cycled over sets
-    idxs = [idx]
-    for i in range(1, args.steps):
-        idxs.append(torch.from_numpy(np.stack([rng.choice(256, 10, replace=False) for _ in range(8)])
-                                     .astype(np.int32)).to(dev))
-    distinct = [int(torch.unique(t).numel()) for t in idxs]
+    idx_np = [wl["idx"]] + [np.stack([rng.choice(256, 10, replace=False) for _ in range(8)]).astype(np.int32)
+                            for _ in range(1, L)]
+    idxs = [idx] + [torch.from_numpy(a).to(dev) for a in idx_np[1:]]
+    distinct = [int(np.unique(a).size) for a in idx_np]
     y = torch.empty(8, 2048, dtype=torch.bfloat16, device=dev)
 
     def mk(i):
@@ -386,9 +489,10 @@ def setup_cfg2(args, dev):
     mean_distinct = float(np.mean(distinct))
     row_bytes = 512 // 2 + 8 * 4
     bytes_ = int(mean_distinct * 2048 * row_bytes + 8 * 10 * 512 * 2 + 8 * 2048 * 2 + 8 * 10 * 4)
-    return wl, [mk(i) for i in range(args.steps)], {
+    return wl, [mk(i) for i in range(L)], {
         "bytes": bytes_, "flops": synth.algorithmic_flops(2, wl), "bound": "hbm",
         "kernel": "down_pair_kernel<16>", "sets": len(sets), "mean_distinct_experts": mean_distinct,
+        "cycle_bytes": L * bytes_,
         "workload": "decode down + top-10 weighted sum: 8 tokens, I=512, D=2048, E=256, "
                     "W [256,2048,512] int4 g64 -> y [8,2048]"}
 
@@ -407,13 +511,18 @@ def _prefill_common(args, dev, cfg):
     return wl, x, sets, r, lhs, out
 
 
+def prefill_steps(args):
+    """Steps per timed window of the prefill workloads (each call ~0.2 ms)."""
+    return max(1, args.steps // 10)
+
+
 def setup_cfg3(args, dev):
     import torch
     from titan_amd import ops, synth
 
     wl, x, sets, r, lhs, out = _prefill_common(args, dev, 3)
     t = r.tiles
-    steps = max(1, args.steps // 10)
+    L = 2 * prefill_steps(args)  # two weight sets of 302 MB alternate: each call reads cold weights
     # load-time repack into the tile layout (outside the timed region)
     tsets = [ops.repack_tiles(w, s, b) for (w, s, b) in sets]
     torch.cuda.synchronize()
@@ -438,10 +547,11 @@ def setup_cfg3(args, dev):
                           out.data_ptr(), torch.cuda.current_stream().cuda_stream)
         return f
 
-    return wl, [mk_tiles(i) for i in range(steps)], {
+    return wl, [mk_tiles(i) for i in range(L)], {
         "flops": synth.algorithmic_flops(3, wl), "bound": "mfma", "peak_tflops": BF16_PEAK_TFLOPS,
-        "kernel": "gemm_bf16_kernel<true, false>", "sets": len(sets),
-        "alt": ("mlx_layout_us_per_call", [mk_mlx(i) for i in range(steps)]),
+        "peak_key": "bf16_mfma_TFLOPs", "kernel": "gemm_bf16_kernel<true, false>", "sets": len(sets),
+        "steps": prefill_steps(args),
+        "alt": ("mlx_layout_us_per_call", [mk_mlx(i) for i in range(L)]),
         "workload": "prefill grouped GEMM: 4096 tokens x top-10 Zipf(1.1) routed rows sorted by expert, "
                     "gate_up W [256,1024,2048] int4 g64 (tile layout, repacked at load), x gathered "
                     "in-kernel -> [40960,1024]"}
@@ -456,7 +566,7 @@ def setup_cfg4(args, dev):
     T = wl.meta["T"]
     xi = torch.empty(T, 2048, dtype=torch.int8, device=dev)
     sx = torch.empty(T, dtype=torch.float32, device=dev)
-    steps = max(1, args.steps // 10)
+    L = 2 * prefill_steps(args)
     # load-time repack into the tile layout (outside the timed region)
     tsets = [ops.repack_tiles(w, s, b) for (w, s, b) in sets]
     torch.cuda.synchronize()
@@ -485,10 +595,11 @@ def setup_cfg4(args, dev):
                           t.ntiles.data_ptr(), t.maxt, out.data_ptr(), st)
         return f
 
-    return wl, [mk(i) for i in range(steps)], {
+    return wl, [mk(i) for i in range(L)], {
         "flops": synth.algorithmic_flops(4, wl), "bound": "mfma", "peak_tflops": INT8_PEAK_TOPS,
-        "kernel": "quant_act_kernel + gemm_int8_kernel<true>", "sets": len(sets),
-        "alt": ("mlx_layout_us_per_call", [mk_mlx(i) for i in range(steps)]),
+        "peak_key": "int8_mfma_TOPs", "kernel": "quant_act_kernel + gemm_int8_kernel<true>", "sets": len(sets),
+        "steps": prefill_steps(args),
+        "alt": ("mlx_layout_us_per_call", [mk_mlx(i) for i in range(L)]),
         "workload": "int8-activation x int4-weight gate_up prefill: 4096 tokens x top-10 Zipf(1.1), "
                     "per-token symmetric int8 x, W [256,1024,2048] int4 g64 (tile layout, repacked at load) "
                     "-> [40960,1024]"}
@@ -500,7 +611,9 @@ def setup_cfg5(args, dev):
     from titan_amd import ops, synth
 
     wl = synth.make(5)
-    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 105)
+    per_call = synth.algorithmic_bytes(5)
+    L = cycle_len(args.steps, per_call, args.rotate_gb * 1e9)
+    sets = weight_sets(wl, min(L, n_sets_needed(wl, L * per_call, args.rotate_gb)), dev, 105)
     x = to_dev(wl["x"], "bf16", dev)
     out = torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
@@ -513,9 +626,9 @@ def setup_cfg5(args, dev):
                           b.data_ptr(), 4096, 64, 8, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
         return f
 
-    return wl, [mk(i) for i in range(args.steps)], {
-        "bytes": synth.algorithmic_bytes(5), "flops": synth.algorithmic_flops(5), "bound": "hbm",
-        "kernel": "qmv_kernel<4, 16, 0, 8>", "sets": len(sets),
+    return wl, [mk(i) for i in range(L)], {
+        "bytes": per_call, "flops": synth.algorithmic_flops(5), "bound": "hbm",
+        "kernel": "qmv_kernel<4, 16, 0, 8>", "sets": len(sets), "cycle_bytes": min(L, len(sets)) * per_call,
         "workload": "dense quantized_matmul x [1,2048] . W [4096,2048] int8 codes g64"}
 
 
@@ -531,20 +644,24 @@ def run_widths(args, dev):
     from titan_amd import ops, synth
 
     wl = synth.make(1)
-    sets = weight_sets(wl, n_sets_for(wl, args.rotate_gb), dev, 106)
+    sets = weight_sets(wl, n_sets_needed(wl, 0, args.rotate_gb), dev, 106)
     tsets = [ops.repack_tiles(w, s, b, swiglu_pairs=True) for (w, s, b) in sets]
     rng = np.random.default_rng(1006)
     per_expert = 2 * 512 * (2048 // 2 + 32 * 4)
     res = {}
+    steps = max(8, args.steps // 2)
     for T in WIDTHS:
         x = to_dev(synth.bf16_bits(rng.normal(size=(T, 2048)).astype(np.float32)), "bf16", dev)
+        n_idx = len(sets)
         idx_np = [np.stack([rng.choice(256, 10, replace=False) for _ in range(T)]).astype(np.int32)
-                  for _ in sets]
+                  for _ in range(n_idx)]
         idx = [torch.from_numpy(a).to(dev) for a in idx_np]
         distinct = float(np.mean([np.unique(a).size for a in idx_np]))
         h = torch.empty(T * 10, 512, dtype=torch.bfloat16, device=dev)
         routes = [ops.route(i, 256) for i in idx]
         lhs = [torch.div(r.order, 10, rounding_mode="floor").to(torch.int32) for r in routes]
+        ws = torch.empty(max(int(ops._lib.load().qmoe_route_workspace_size(T * 10, 256)), 256) // 4,
+                         dtype=torch.int32, device=dev)
         torch.cuda.synchronize()
 
         def mk_dec(i, T=T, x=x, idx=idx, h=h):
@@ -557,12 +674,10 @@ def run_widths(args, dev):
                               torch.cuda.current_stream().cuda_stream)
             return f
 
-        def mk_sorted(i, T=T, x=x, h=h):
+        def mk_sorted(i, T=T, x=x, h=h, ws=ws):
             j = i % len(sets)
             tw, r, lh = tsets[j], routes[j], lhs[j]
             t = r.tiles
-            ws = torch.empty(max(int(ops._lib.load().qmoe_route_workspace_size(T * 10, 256)), 256) // 4,
-                             dtype=torch.int32, device=dev)
             flat = idx[j].reshape(-1)
 
             def f():
@@ -577,10 +692,9 @@ def run_widths(args, dev):
                               h.data_ptr(), st)
             return f
 
-        steps = max(8, args.steps // 2)
-        sec_d, _ = (time_eager if args.eager else time_graph)([mk_dec(i) for i in range(steps)], args.warmup, dev)
-        sec_s, _ = (time_eager if args.eager else time_graph)([mk_sorted(i) for i in range(steps)], args.warmup,
-                                                              dev)
+        L = steps * int(np.ceil(len(sets) / steps))
+        sec_d, _ = timer(args)([mk_dec(i) for i in range(L)], steps, args.warmup, dev)
+        sec_s, _ = timer(args)([mk_sorted(i) for i in range(L)], steps, args.warmup, dev)
         nbytes = distinct * per_expert + T * 2048 * 2 + T * 10 * 512 * 2
         res[T] = {"pairs": T * 10, "distinct_experts": distinct, "decode_us": round(sec_d * 1e6, 3),
                   "decode_GBps": round(nbytes / sec_d / 1e9, 1), "sorted_us": round(sec_s * 1e6, 3),
@@ -620,9 +734,10 @@ def run_block(args, dev):
         blocks = [block() for _ in range(nblocks)]
         x = to_dev(synth.bf16_bits(rng.normal(size=(T, 2048)).astype(np.float32)), "bf16", dev)
         torch.cuda.synchronize()
-        steps = args.steps if T == 1 else max(1, args.steps // 10)
-        fns = [(lambda b=blocks[i % nblocks]: b(x)) for i in range(steps)]
-        sec, tinfo = (time_eager if args.eager else time_graph)(fns, args.warmup if T == 1 else 2, dev)
+        steps = args.steps if T == 1 else prefill_steps(args)
+        L = steps * int(np.ceil(nblocks / steps))
+        fns = [(lambda b=blocks[i % nblocks]: b(x)) for i in range(L)]
+        sec, tinfo = timer(args)(fns, steps, args.warmup if T == 1 else 2, dev)
         r = {"us_per_call": round(sec * 1e6, 3), "us_per_call_min": round(tinfo["min"] * 1e6, 3)}
         if T == 1:
             nbytes = 256 * 2048 * 2 + 10 * (per_gu + per_dn) + 2048 * 2 * 2
@@ -648,27 +763,62 @@ SETUPS = {0: setup_cfg0, 1: setup_cfg1, 2: setup_cfg2, 3: setup_cfg3, 4: setup_c
 # ------------------------------------------------------------- CPU baseline
 
 
+def cpu_threads():
+    """Threads the CPU legs use: this process's CPU affinity, capped by
+    OMP_NUM_THREADS when that is set (the host's share of cores)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return n
+
+
 def cpu_baseline(cfg, wl, budget_s):
-    """The oracle (C, OpenMP) on the same seeded inputs, timed on this host."""
+    """The oracle (C, OpenMP, fp64 accumulation) on the same seeded inputs,
+    timed on this host; the prefill workloads on a sample of their routed rows."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
     from titan_amd import synth
 
     oracle.build()
-    threads = oracle.max_threads()
+    nt = cpu_threads()
     if cfg == 1:
         def run():
             gu, _ = oracle.gather_qmm_rows(wl["x"], np.zeros(10, np.int32), wl["idx"].reshape(-1), wl["w"],
-                                           wl["s"], wl["b"])
+                                           wl["s"], wl["b"], n_threads=nt)
             oracle.swiglu(gu)
-        work, unit = synth.algorithmic_bytes(1), "GB/s"
-        sample = "full workload: 10 experts x 1024 rows x 2048, fp64 accumulation"
+        work, unit, scale = synth.algorithmic_bytes(1), "GB/s", 1e9
+        sample = "full workload: 10 experts x 1024 rows x 2048 + SwiGLU"
     elif cfg == 0:
         def run():
             oracle.gather_qmm_rows(wl["x"], None, np.zeros(1, np.int32), wl["w"][None], wl["s"][None],
-                                   wl["b"][None])
-        work, unit = synth.algorithmic_bytes(0), "GB/s"
-        sample = "full workload"
+                                   wl["b"][None], n_threads=nt)
+        work, unit, scale = synth.algorithmic_bytes(0), "GB/s", 1e9
+        sample = "full workload: 4096 rows x 2048"
+    elif cfg == 2:
+        def run():
+            oracle.down_wsum(wl["h"], wl["idx"], wl["scores"], wl["w"], wl["s"], wl["b"], n_threads=nt)
+        work, unit, scale = synth.algorithmic_bytes(2, wl), "GB/s", 1e9
+        sample = "full workload: 8 tokens x 10 experts x 2048 rows x 512 + weighted sum"
+    elif cfg in (3, 4):
+        T, k = wl["idx"].shape
+        rows = np.random.default_rng(cfg).choice(T * k, size=256, replace=False)
+        order, _, srt = oracle.route_sort(wl["idx"], 256)
+        xr = (order[rows] // k).astype(np.int32)
+        ex = srt[rows]
+        if cfg == 3:
+            def run():
+                oracle.gather_qmm_rows(wl["x"], xr, ex, wl["w"], wl["s"], wl["b"], deq="bf16", n_threads=nt)
+            sample = "256 of the 40960 routed rows x 1024 columns x 2048 (bf16-dequantised weights)"
+        else:
+            toks = np.unique(xr)
+
+            def run():
+                xi, sx = oracle.quant_act_int8(wl["x"][toks])
+                remap = np.searchsorted(toks, xr).astype(np.int32)
+                oracle.gather_qmm_int8_rows(xi, sx, remap, ex, wl["w"], wl["s"], wl["b"], n_threads=nt)
+            sample = "256 of the 40960 routed rows x 1024 columns x 2048, with their tokens' int8 quantisation"
+        work, unit, scale = 2 * 256 * 1024 * 2048, "TFLOP/s" if cfg == 3 else "TOP/s", 1e12
     else:
         return None
     run()
@@ -680,8 +830,9 @@ def cpu_baseline(cfg, wl, budget_s):
         if el > budget_s or reps >= 1000:
             break
     per = el / reps
-    return {"value": round(work / per / 1e9, 3), "unit": unit, "cores": threads, "kind": "port",
-            "sample": f"{sample}; {reps} repetitions in {el:.1f} s; {per * 1e3:.2f} ms per call",
+    return {"value": round(work / per / scale, 4), "unit": unit, "cores": nt, "kind": "port",
+            "affinity_cores": len(os.sched_getaffinity(0)),
+            "sample": f"{sample}; {reps} repetitions in {el:.1f} s; {per * 1e3:.3f} ms per call",
             "cpu": _cpu_model()}
 
 
@@ -718,69 +869,99 @@ def main():
         return 0
     if args.only is not None:
         cfgs = [int(args.only)]
+    peaks = None
+    if args.only is None and not args.no_peaks:
+        print("[bench] measured peaks", file=sys.stderr, flush=True)
+        peaks = measure_peaks(dev)
+        print(f"[bench] peaks: {peaks}", file=sys.stderr, flush=True)
     results = {}
     head = None
+    wls = {}
     for cfg in cfgs:
         print(f"[bench] workload {cfg}: setup", file=sys.stderr, flush=True)
         if cfg in (6, 7):
             results[cfg] = (run_widths if cfg == 6 else run_block)(args, dev)
             torch.cuda.empty_cache()
             continue
-        wl, fns, meta = SETUPS[cfg](args, dev)
-        print(f"[bench] workload {cfg}: timing {len(fns)} steps", file=sys.stderr, flush=True)
-        sec, tinfo = (time_eager if args.eager else time_graph)(fns, args.warmup, dev)
+        wl, cycle, meta = SETUPS[cfg](args, dev)
+        wls[cfg] = wl
+        steps = meta.get("steps", args.steps)
+        print(f"[bench] workload {cfg}: timing {len(cycle)} launches in windows of {steps}", file=sys.stderr,
+              flush=True)
+        sec, tinfo = timer(args)(cycle, steps, args.warmup, dev)
         res = {"workload": meta["workload"], "us_per_call": round(sec * 1e6, 3),
-               "us_per_call_min": round(tinfo["min"] * 1e6, 3), "timed_rounds": tinfo["rounds"],
+               "us_per_call_min": round(tinfo["min"] * 1e6, 3), "us_per_call_max": round(tinfo["max"] * 1e6, 3),
+               "timed_rounds": tinfo["rounds"], "steps_per_round": steps, "cycle_launches": len(cycle),
                "kernel": meta["kernel"], "weight_sets": meta["sets"]}
         if meta["bound"] == "hbm":
             gbs = meta["bytes"] / sec / 1e9
             res.update(metric="HBM GB/s", value=round(gbs, 1), bytes_per_call=meta["bytes"],
-                       pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2))
+                       pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2),
+                       touched_bytes_per_round=int(steps * meta["bytes"]),
+                       rotation_bytes_per_cycle=int(meta["cycle_bytes"]))
+            if peaks:
+                res["pct_measured_hbm_read"] = round(100 * gbs / peaks["hbm_read_GBps"], 2)
         else:
             tf = meta["flops"] / sec / 1e12
             res.update(metric="TFLOP/s" if cfg == 3 else "TOP/s", value=round(tf, 1),
                        flops_per_call=meta["flops"], pct_peak=round(100 * tf / meta["peak_tflops"], 2),
                        pct_bf16_peak=round(100 * tf / BF16_PEAK_TFLOPS, 2))
+            if peaks:
+                res["pct_measured_peak"] = round(100 * tf / peaks[meta["peak_key"]], 2)
         for k_ in ("mean_distinct_experts",):
             if k_ in meta:
                 res[k_] = meta[k_]
         if "alt" in meta:
             label, alt = meta["alt"]
-            sec_alt, _ta = (time_eager if args.eager else time_graph)(alt, args.warmup, dev)
+            sec_alt, _ta = timer(args)(alt, steps, args.warmup, dev)
             res[label] = round(sec_alt * 1e6, 3)
             del alt, _ta
         results[cfg] = res
         print(f"[bench] workload {cfg}: {res}", file=sys.stderr, flush=True)
         if cfg == 1:
             head = (wl, meta, sec)
-        del fns, tinfo
+        del cycle, tinfo
         torch.cuda.empty_cache()
     if args.only is not None:
         return 0
+    peaks_after = None
+    if peaks is not None:
+        peaks_after = measure_peaks(dev)
+        print(f"[bench] peaks after the workloads: {peaks_after}", file=sys.stderr, flush=True)
     if head is None:
-        print(json.dumps({"configs": results}))
+        print(json.dumps({"configs": results, "peaks_measured": peaks}))
         return 0
     wl, meta, sec = head
     gbs = meta["bytes"] / sec / 1e9
     if traffic is None:
         traffic = traffic_from_profile()
-    cpu = None
+    cpu, cpu_rows = None, {}
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(1, wl, args.cpu_seconds)
+        for c in (0, 2, 3, 4):
+            if c in cfgs:
+                cpu_rows[c] = cpu_baseline(c, wls[c], args.cpu_seconds / 3)
+                print(f"[bench] cpu baseline {c}: {cpu_rows[c]}", file=sys.stderr, flush=True)
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None if traffic is None else round(traffic["bytes"]),
+            "kernel": TRAFFIC_KERNEL, "bytes_per_launch": meta["bytes"], "traffic_detail": traffic}
+    if peaks:
+        roof["peak_measured"] = peaks["hbm_read_GBps"]
+        roof["frac_measured"] = round(gbs / peaks["hbm_read_GBps"], 4)
     line = {
         "metric": METRIC,
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(sec * 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": meta["workload"], "tokens": 1, "top_k": 10, "experts": 256, "hidden": 2048,
-                   "intermediate": 512, "group_size": 64, "bits": 4, "weight_sets_rotated": meta["sets"]},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None if traffic is None else round(traffic["bytes"]),
-                     "kernel": TRAFFIC_KERNEL, "bytes_per_launch": meta["bytes"],
-                     "traffic_detail": traffic},
+                   "intermediate": 512, "group_size": 64, "bits": 4, "weight_sets_rotated": meta["sets"],
+                   "timing": "median per step over the timed windows of exactly `steps` launches"},
+        "roofline": roof,
         "cpu_baseline": cpu,
+        "cpu_baseline_configs": cpu_rows,
+        "peaks_measured": {"before": peaks, "after": peaks_after},
         "configs": results,
     }
     print(json.dumps(line))

@@ -1,0 +1,38 @@
+/*
+ * qmoe_peaks.h -- measured-ceiling probes for MI355X (libqmoe_peaks.so).
+ *
+ * Not part of the MoE path: bench.py times these to report its roofline
+ * fractions against what this part sustains as well as against the vendor
+ * figures (the reference's method: measure the device's own peaks with a
+ * read kernel and a matrix-unit loop, engine/patches/prefill-int4/peak_table.py:1-30).
+ * Same conventions as qmoe.h: device pointers, caller-owned buffers, launches
+ * on `stream`, no host synchronisation, 0 on success.
+ */
+#ifndef QMOE_PEAKS_H
+#define QMOE_PEAKS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Reads `bytes` (a multiple of 16, 16-byte aligned) once with 16-byte
+ * non-temporal loads from every CU; folds what it read into sink[block]
+ * (sink holds qmoe_peak_stream_blocks() words) so nothing is optimised away. */
+int qmoe_peak_stream_blocks(void);
+int qmoe_peak_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+
+/* Dense matrix-unit loops over register operands seeded per lane:
+ * qmoe_peak_mfma_waves() waves each issue `iters` x 4 independent
+ * v_mfma_f32_32x32x16_bf16 (32768 flops each) or v_mfma_i32_32x32x32_i8
+ * (65536 ops each).  sink holds one word per wave. */
+int qmoe_peak_mfma_waves(void);
+int qmoe_peak_mfma_bf16(int iters, uint32_t* sink, void* stream);
+int qmoe_peak_mfma_i8(int iters, uint32_t* sink, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMOE_PEAKS_H */

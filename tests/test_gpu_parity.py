@@ -589,3 +589,106 @@ def test_decode_gemv_tail_chunk_shapes(dev, orc, K):
     yq = ops.quantized_matmul(bf16_t(x, dev), words_t(w[0], dev), bf16_t(s[0], dev), bf16_t(b[0], dev))
     refq, _ = orc.gather_qmm_rows(x, None, np.zeros(2, np.int32), w[:1], s[:1], b[:1])
     assert_close_bf16(orc, bits(yq), refq, what=f"quantized_matmul K={K}")
+
+
+# ------------------------------------- timed kernels at their timed shapes
+
+
+def _prefill_routed(dev, orc, tokens, cfg=3):
+    """A Zipf-routed prefill workload, routed on the device: (workload, routing,
+    x_rows = order // k, host order, host sorted ids, host offsets)."""
+    wl = synth.make(cfg, tokens=tokens)
+    k = wl["idx"].shape[1]
+    r = ops.route(i32_t(wl["idx"], dev), 256)
+    lhs = torch.div(r.order, k, rounding_mode="floor").to(torch.int32)
+    order, _, srt = orc.route_sort(wl["idx"], 256)
+    off = np.searchsorted(srt, np.arange(257), side="left")
+    return wl, r, lhs, order, srt, off
+
+
+@pytest.mark.parametrize("tokens", [4096, 8192])
+def test_sorted_gemm_tiles_prefill_sampled(dev, orc, tokens):
+    """The tile-layout grouped GEMM the bench times for workload 3, at its
+    full size (4096 tokens, 477 tiles) and at 8192 tokens, where the tile
+    count passes the 512 the heavy-first ranking holds and the kernel walks
+    tiles in table order."""
+    say(f"sorted GEMM tiles, {tokens} tokens x top-10 Zipf, sampled rows")
+    wl, r, lhs, order, srt, off = _prefill_routed(dev, orc, tokens)
+    T, k = wl["idx"].shape
+    nt = int(r.tiles.ntiles.item())
+    assert (nt > 512) == (tokens == 8192), nt
+    tw = ops.repack_tiles(words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev))
+    y = ops.gather_qmm_sorted_tiles(bf16_t(wl["x"], dev), tw, r.tiles, x_rows=lhs)
+    torch.cuda.synchronize()
+    rows = _sample_rows(off, T * k, 384, np.random.default_rng(tokens))
+    ref64, _ = orc.gather_qmm_rows(wl["x"], (order[rows] // k).astype(np.int32), srt[rows], wl["w"], wl["s"],
+                                   wl["b"], deq="bf16")
+    assert_close_bf16(orc, bits(y)[rows], ref64, what=f"gemm tiles {tokens} tokens, {nt} tiles, {rows.size} rows")
+    if tokens == 8192:
+        # the MLX-layout kernel's unranked branch, same rows and summation order
+        ym = ops.gather_qmm_sorted(bf16_t(wl["x"], dev), words_t(wl["w"], dev), bf16_t(wl["s"], dev),
+                                   bf16_t(wl["b"], dev), r.tiles, x_rows=lhs)
+        assert torch.equal(ym, y)
+
+
+@pytest.mark.parametrize("tokens", [4096, 8192])
+def test_swiglu_gemm_tiles_prefill_sampled(dev, orc, tokens):
+    """The SwiGLU-epilogue grouped GEMM (the block's prefill gate_up) at the
+    workload-3 shape and past 512 tiles: h = silu(gate) * up against the
+    fp64 closed form over bf16-dequantised weights."""
+    say(f"SwiGLU GEMM tiles, {tokens} tokens x top-10 Zipf, sampled rows")
+    wl, r, lhs, order, srt, off = _prefill_routed(dev, orc, tokens)
+    T, k = wl["idx"].shape
+    tw = ops.repack_tiles(words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev), swiglu_pairs=True)
+    h = ops.gather_qmm_swiglu_sorted_tiles(bf16_t(wl["x"], dev), tw, r.tiles, x_rows=lhs)
+    torch.cuda.synchronize()
+    assert h.shape == (T * k, 512)
+    rows = _sample_rows(off, T * k, 256, np.random.default_rng(tokens + 1))
+    gu64, _ = orc.gather_qmm_rows(wl["x"], (order[rows] // k).astype(np.int32), srt[rows], wl["w"], wl["s"],
+                                  wl["b"], deq="bf16")
+    h64, _ = orc.swiglu(gu64)
+    assert_close_bf16(orc, bits(h)[rows], h64, what=f"swiglu gemm {tokens} tokens, {rows.size} rows")
+
+
+def test_sorted_gemm_int8_tiles_past_512_tiles(dev, orc):
+    """The int8 grouped GEMM over 8192 tokens (more than 512 tiles: tiles in
+    table order), sampled rows against the fake-quant golden."""
+    say("int8 sorted GEMM tiles, 8192 tokens, sampled rows")
+    wl, r, lhs, order, srt, off = _prefill_routed(dev, orc, 8192, cfg=4)
+    T, k = wl["idx"].shape
+    assert int(r.tiles.ntiles.item()) > 512
+    xi, sx = ops.quantize_act_int8(bf16_t(wl["x"], dev))
+    tw = ops.repack_tiles(words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev))
+    y = ops.gather_qmm_int8_sorted_tiles(xi, sx, tw, r.tiles, x_rows=lhs)
+    torch.cuda.synchronize()
+    rows = _sample_rows(off, T * k, 256, np.random.default_rng(3))
+    rxi, rsx = orc.quant_act_int8(wl["x"])
+    ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, (order[rows] // k).astype(np.int32), srt[rows], wl["w"],
+                                        wl["s"], wl["b"])
+    assert_close_bf16(orc, bits(y)[rows], ref64, what=f"int8 gemm 8192 tokens, {rows.size} rows")
+
+
+@pytest.mark.parametrize("gs", [32, 128])
+def test_fused_decode_group_sizes(dev, orc, gs):
+    """The fused decode kernels (gate_up + SwiGLU, down + weighted sum) with
+    group sizes 32 and 128 at the workload shapes: the reference's fused decode
+    path takes group 64 and 128 (engine/patches/decode-fusion/kernel.py:50-60)."""
+    say(f"fused decode gate_up / down group_size={gs}")
+    rng = np.random.default_rng(gs)
+    E, I, K, T, k = 256, 512, 2048, 3, 10
+    w, s, b = synth.quant_weights(rng, (E, 2 * I), K, group_size=gs)
+    x = synth.bf16_bits(rng.normal(size=(T, K)).astype(np.float32))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    h = ops.gate_up_silu(bf16_t(x, dev), words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), i32_t(idx, dev),
+                         group_size=gs)
+    gu64, _ = orc.gather_qmm_rows(x, np.repeat(np.arange(T), k).astype(np.int32), idx.reshape(-1), w, s, b,
+                                  group_size=gs)
+    h64, _ = orc.swiglu(gu64)
+    assert_close_bf16(orc, bits(h).reshape(T * k, I), h64, what=f"gate_up gs{gs}")
+    wd, sd, bd = synth.quant_weights(rng, (E, K), I, group_size=gs)
+    sc = synth.softmax(rng.normal(size=(T, k)))
+    for TT in (1, T):  # one token: the 8-row variant; more: the 16-row one
+        y = ops.down_wsum(h[:TT], words_t(wd, dev), bf16_t(sd, dev), bf16_t(bd, dev), i32_t(idx[:TT], dev),
+                          f32_t(sc[:TT], dev), group_size=gs)
+        y64, _ = orc.down_wsum(bits(h[:TT]), idx[:TT], sc[:TT], wd, sd, bd, group_size=gs)
+        assert_close_bf16(orc, bits(y), y64, what=f"down gs{gs} T={TT}")

@@ -85,3 +85,19 @@ def test_check_maps_codes_to_exceptions(L):
         _lib.call("qmoe_weighted_sum", 16, None, 16, 2, 10, 256, 9, 16, None)
     with pytest.raises(_lib.QmoeError):
         _lib.call("qmoe_weighted_sum", None, None, None, 2, 10, 256, 2, None, None)
+
+
+def test_peaks_library_exports_its_header():
+    """libqmoe_peaks.so (the bench's measured-ceiling probes) exports what
+    include/qmoe_peaks.h declares."""
+    from titan_amd import build
+
+    if not build.PEAKS_LIB.exists():
+        build.build()
+    names = sorted(set(re.findall(r"\b(qmoe_peak_[a-z0-9_]+)\s*\(", (ROOT / "include" / "qmoe_peaks.h").read_text())))
+    out = subprocess.run(["nm", "-D", "--defined-only", str(build.PEAKS_LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (qmoe_peak_[a-z0-9_]+)$", out, flags=re.M))
+    assert names and set(names) <= exported, (names, exported)
+    L = ctypes.CDLL(str(build.PEAKS_LIB))
+    assert L.qmoe_peak_stream_blocks() > 0 and L.qmoe_peak_mfma_waves() > 0

@@ -1,8 +1,10 @@
 """Build libqmoe.so (the gfx950 kernels behind include/qmoe.h) with hipcc.
 
 Each ``csrc/*.hip`` file is compiled to an object in parallel, then linked into
-``titan_amd/lib/libqmoe.so``.  The library lands in-tree so that it travels
-with the source tree; nothing is installed anywhere else.
+``titan_amd/lib/libqmoe.so``; ``csrc/peaks/peaks.hip`` (the bench's
+measured-ceiling probes, include/qmoe_peaks.h) becomes
+``titan_amd/lib/libqmoe_peaks.so``.  The libraries land in-tree so that they
+travel with the source tree; nothing is installed anywhere else.
 
     python -m titan_amd.build            # build (always recompiles)
 """
@@ -23,6 +25,8 @@ INCLUDE = ROOT / "include"
 BUILD = PKG / "_build"
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libqmoe.so"
+PEAKS_SRC = CSRC / "peaks" / "peaks.hip"
+PEAKS_LIB = LIB_DIR / "libqmoe_peaks.so"
 ARCH = os.environ.get("QMOE_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
@@ -55,21 +59,28 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    BUILD.mkdir(exist_ok=True)
-    LIB_DIR.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
-    jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
-    with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs, lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    jobs = min(len(sources) + 1, max(1, min(8, os.cpu_count() or 1)))
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        fut_peaks = ex.submit(_compile, PEAKS_SRC)
+        objs = list(ex.map(_compile, sources))
+        peaks_obj = fut_peaks.result()
+    _link(objs, LIB)
+    _link([peaks_obj], PEAKS_LIB)
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources")
+        print(f"built {LIB} from {len(sources)} sources and {PEAKS_LIB}")
     return LIB
 
 

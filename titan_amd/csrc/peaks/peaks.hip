@@ -1,0 +1,133 @@
+// Ceiling probes for the bench's measured-peak denominators (qmoe_peaks.h):
+// a streaming read over a buffer larger than the caches and dense MFMA loops.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qmoe_peaks.h"
+
+namespace {
+
+constexpr int kStreamThreads = 256;
+constexpr int kStreamBlocks = 256 * 8;  // eight blocks per CU
+constexpr int kUnroll = 8;              // 16-byte loads in flight per thread
+
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((__vector_size__(16 * sizeof(int)))) int i32x16_t;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+
+__global__ __launch_bounds__(kStreamThreads) void stream_read_kernel(const i32x4_t* __restrict__ p, int64_t n,
+                                                                     uint32_t* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * kStreamThreads;
+  int64_t i = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + (kUnroll - 1) * stride < n; i += kUnroll * stride) {
+    i32x4_t v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(p + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc ^= (uint32_t)(v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3]);
+  }
+  for (; i < n; i += stride) {
+    const i32x4_t v = __builtin_nontemporal_load(p + i);
+    acc ^= (uint32_t)(v[0] ^ v[1] ^ v[2] ^ v[3]);
+  }
+  // one word per block: the block's xor, written by thread 0
+  __shared__ uint32_t red[kStreamThreads / 64];
+  for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m, 64);
+  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+constexpr int kMfmaThreads = 256;
+constexpr int kMfmaBlocks = 256 * 2;  // two blocks of four waves per CU: two waves per SIMD
+
+__device__ __forceinline__ uint32_t mix(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352dU;
+  x ^= x >> 15;
+  x *= 0x846ca68bU;
+  x ^= x >> 16;
+  return x;
+}
+
+// Random bf16 operands in [-2, 2) (exponent kept in range so no value is
+// special): the matrix core's power, and so the sustained clock, depends on
+// the data it multiplies.
+__device__ __forceinline__ bf16x8_t rand_bf16x8(uint32_t seed) {
+  i32x4_t r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t h = mix(seed * 4 + j);
+    r[j] = (int)((h & 0x807F807Fu) | 0x3F003F00u);  // sign, 7 mantissa bits, exponents 2^-1 .. 2^0
+  }
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+__global__ __launch_bounds__(kMfmaThreads) void mfma_bf16_kernel(int iters, uint32_t* __restrict__ sink) {
+  const uint32_t gid = blockIdx.x * kMfmaThreads + threadIdx.x;
+  const bf16x8_t a0 = rand_bf16x8(gid * 4 + 0), a1 = rand_bf16x8(gid * 4 + 1);
+  const bf16x8_t b0 = rand_bf16x8(gid * 4 + 2), b1 = rand_bf16x8(gid * 4 + 3);
+  f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  for (int it = 0; it < iters; ++it) {
+    c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, c1, 0, 0, 0);
+    c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, c2, 0, 0, 0);
+    c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, c3, 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s += c0[r] + c1[r] + c2[r] + c3[r];
+  if (threadIdx.x % 64 == 0) sink[gid / 64] = __float_as_uint(s);
+}
+
+__global__ __launch_bounds__(kMfmaThreads) void mfma_i8_kernel(int iters, uint32_t* __restrict__ sink) {
+  const uint32_t gid = blockIdx.x * kMfmaThreads + threadIdx.x;
+  i32x4_t a0, a1, b0, b1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a0[j] = (int)mix(gid * 16 + j);
+    a1[j] = (int)mix(gid * 16 + 4 + j);
+    b0[j] = (int)mix(gid * 16 + 8 + j);
+    b1[j] = (int)mix(gid * 16 + 12 + j);
+  }
+  i32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  for (int it = 0; it < iters; ++it) {
+    c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, c1, 0, 0, 0);
+    c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, c2, 0, 0, 0);
+    c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, c3, 0, 0, 0);
+  }
+  int s = 0;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s += c0[r] ^ c1[r] ^ c2[r] ^ c3[r];
+  if (threadIdx.x % 64 == 0) sink[gid / 64] = (uint32_t)s;
+}
+
+int status() { return hipGetLastError() == hipSuccess ? 0 : 3; }
+
+}  // namespace
+
+extern "C" int qmoe_peak_stream_blocks(void) { return kStreamBlocks; }
+
+extern "C" int qmoe_peak_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
+  if (!buf || !sink || bytes % 16 || (reinterpret_cast<uintptr_t>(buf) & 15)) return 1;
+  stream_read_kernel<<<dim3(kStreamBlocks), dim3(kStreamThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const i32x4_t*>(buf), (int64_t)(bytes / 16), sink);
+  return status();
+}
+
+extern "C" int qmoe_peak_mfma_waves(void) { return kMfmaBlocks * kMfmaThreads / 64; }
+
+extern "C" int qmoe_peak_mfma_bf16(int iters, uint32_t* sink, void* stream) {
+  if (iters <= 0 || !sink) return 1;
+  mfma_bf16_kernel<<<dim3(kMfmaBlocks), dim3(kMfmaThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(iters, sink);
+  return status();
+}
+
+extern "C" int qmoe_peak_mfma_i8(int iters, uint32_t* sink, void* stream) {
+  if (iters <= 0 || !sink) return 1;
+  mfma_i8_kernel<<<dim3(kMfmaBlocks), dim3(kMfmaThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(iters, sink);
+  return status();
+}
