@@ -86,6 +86,25 @@ int qmoe_route(const int32_t* ids, int64_t n_pairs, int32_t num_experts,
                int32_t* tile_exp, int32_t* ntiles, int64_t max_tiles,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* qmoe_route without a caller workspace.  No counterpart in the reference:
+ * this is for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops or harnesses that forbid hipMalloc).  The
+ * routing workspace is a file-scope device array of
+ * QMOE_ROUTE_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held
+ * until the process ends; the entry point calls no allocator.  Calls whose
+ * qmoe_route_workspace_size(n_pairs, num_experts) exceeds it return
+ * QMOE_ERR_UNSUPPORTED (at 256 experts: up to 1,043,456 pairs).  Every call
+ * on one GPU shares that GPU's array, so calls that overlap on one GPU (two
+ * streams, two host threads) race; serialise them.  The stream must belong
+ * to the current device.  Outputs as for qmoe_route; the count of ids
+ * outside [0, E) goes to n_bad[0] when n_bad is not NULL. */
+#define QMOE_ROUTE_NOALLOC_SCRATCH_BYTES (1u << 20)
+int qmoe_route_noalloc(const int32_t* ids, int64_t n_pairs, int32_t num_experts,
+                       int32_t tile_rows, int32_t* order, int32_t* inv_order,
+                       int32_t* sorted_ids, int32_t* offsets, int32_t* tile_row,
+                       int32_t* tile_exp, int32_t* ntiles, int64_t max_tiles,
+                       int32_t* n_bad, void* stream);
+
 /* build_tiles over ids that are already sorted ascending
  * (titan/kernels/moe_gather_ws.py:133-156,181-202). */
 int qmoe_build_tiles(const int32_t* sorted_ids, int64_t n_rows,

@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple] = {
     "qmoe_dequantize": (INT, [P, P, P, I64, I64, INT, INT, P, P]),
     "qmoe_route_workspace_size": (SZ, [I64, I32]),
     "qmoe_route": (INT, [P, I64, I32, I32, P, P, P, P, P, P, P, I64, P, SZ, P]),
+    "qmoe_route_noalloc": (INT, [P, I64, I32, I32, P, P, P, P, P, P, P, I64, P, P]),
     "qmoe_build_tiles": (INT, [P, I64, I32, I32, P, P, P, P, I64, P]),
     "qmoe_gather_qmv": (INT, [P, P, P, I64, I64, P, P, P, I32, I64, INT, INT, P, P]),
     "qmoe_quantized_matmul": (INT, [P, I64, I64, P, P, P, I64, INT, INT, P, P]),

@@ -16,6 +16,8 @@
 //           so a row's slot is its chunk base, plus the rows of its id in the
 //           chunk's earlier quarters, plus the earlier rows of its id in its
 //           own quarter -- a stable sort with no atomics.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -385,6 +387,12 @@ __global__ __launch_bounds__(kScanThreads) void route_fused_kernel(
 
 int64_t n_chunks(int64_t n) { return (n + kChunk - 1) / kChunk; }
 
+// The routing launches, given a workspace of qmoe_route_workspace_size bytes
+// (word 0 unused when `bad` points elsewhere, then (E + 1) * chunks counts).
+int route_launch(const int32_t* ids, int64_t n_pairs, int32_t num_experts, int32_t tile_rows, int32_t* order,
+                 int32_t* inv_order, int32_t* sorted_ids, int32_t* offsets, int32_t* tile_row, int32_t* tile_exp,
+                 int32_t* ntiles, int64_t max_tiles, int32_t* ws, int32_t* bad, hipStream_t st);
+
 }  // namespace
 
 extern "C" size_t qmoe_route_workspace_size(int64_t n_pairs, int32_t num_experts) {
@@ -407,10 +415,17 @@ extern "C" int qmoe_route(const int32_t* ids, int64_t n_pairs, int32_t num_exper
   const size_t need = qmoe_route_workspace_size(n_pairs, num_experts);
   if (!workspace || workspace_bytes < need)
     return qmoe::fail(QMOE_ERR_WORKSPACE, "route needs %zu workspace bytes", need);
-  hipStream_t st = qmoe::as_stream(stream);
-  const int64_t nch = n_chunks(n_pairs);
   int32_t* ws = static_cast<int32_t*>(workspace);
-  int32_t* bad = ws;
+  return route_launch(ids, n_pairs, num_experts, tile_rows, order, inv_order, sorted_ids, offsets, tile_row,
+                      tile_exp, ntiles, max_tiles, ws, ws, qmoe::as_stream(stream));
+}
+
+namespace {
+
+int route_launch(const int32_t* ids, int64_t n_pairs, int32_t num_experts, int32_t tile_rows, int32_t* order,
+                 int32_t* inv_order, int32_t* sorted_ids, int32_t* offsets, int32_t* tile_row, int32_t* tile_exp,
+                 int32_t* ntiles, int64_t max_tiles, int32_t* ws, int32_t* bad, hipStream_t st) {
+  const int64_t nch = n_chunks(n_pairs);
   int32_t* counts = ws + 64;
   if (n_pairs <= kFusedMaxN && num_experts <= kFusedMaxE) {
     int nbits = 1;
@@ -442,6 +457,8 @@ extern "C" int qmoe_route(const int32_t* ids, int64_t n_pairs, int32_t num_exper
   return qmoe::launch_status("route_scatter_kernel");
 }
 
+}  // namespace
+
 extern "C" int qmoe_build_tiles(const int32_t* sorted_ids, int64_t n_rows, int32_t num_experts,
                                 int32_t tile_rows, int32_t* offsets, int32_t* tile_row, int32_t* tile_exp,
                                 int32_t* ntiles, int64_t max_tiles, void* stream) {
@@ -453,4 +470,70 @@ extern "C" int qmoe_build_tiles(const int32_t* sorted_ids, int64_t n_rows, int32
   tiles_from_sorted_kernel<<<dim3(1), dim3(kScanThreads), 0, qmoe::as_stream(stream)>>>(
       sorted_ids, n_rows, num_experts, tile_rows, offsets, tile_row, tile_exp, ntiles, max_tiles);
   return qmoe::launch_status("tiles_from_sorted_kernel");
+}
+
+// ------------------------------------------------------------------------
+// qmoe_route_noalloc: qmoe_route with its workspace in a file-scope device
+// array instead of caller memory, for callers that cannot allocate (code
+// under graph capture, serving loops that forbid allocation).  Each GPU the
+// library runs on holds its own copy of the array until the process ends;
+// every call on that GPU shares it, so calls that overlap on one GPU race.
+// Nothing in it has to start at zero: the count launch writes every
+// (expert, chunk) count it later reads, and the out-of-range count is
+// written to the caller's n_bad (or, when that is null, to word 0).
+static __device__ __align__(256) int32_t scratch[QMOE_ROUTE_NOALLOC_SCRATCH_BYTES / sizeof(int32_t)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch[kMaxDevices];  // device address of `scratch` per device, once looked up
+
+// The device address of this device's `scratch`: looked up once per device,
+// on the first call there, with that device current.  The array's host-side
+// name is only a handle for the runtime, never a device address.
+int scratch_for_device(int dev, int32_t** out) {
+  if (dev < 0 || dev >= kMaxDevices) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return qmoe::fail(QMOE_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch[dev];
+  return QMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int qmoe_route_noalloc(const int32_t* ids, int64_t n_pairs, int32_t num_experts, int32_t tile_rows,
+                                  int32_t* order, int32_t* inv_order, int32_t* sorted_ids, int32_t* offsets,
+                                  int32_t* tile_row, int32_t* tile_exp, int32_t* ntiles, int64_t max_tiles,
+                                  int32_t* n_bad, void* stream) {
+  if (n_pairs < 0 || num_experts <= 0 || tile_rows <= 0 || max_tiles < 0)
+    return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (num_experts > 8192) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "num_experts=%d > 8192", num_experts);
+  if (n_pairs > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "too many pairs");
+  const size_t need = qmoe_route_workspace_size(n_pairs, num_experts);
+  if (need > QMOE_ROUTE_NOALLOC_SCRATCH_BYTES)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED,
+                      "n_pairs=%lld with %d experts needs %zu scratch bytes; the static scratch holds %zu "
+                      "(use qmoe_route with a workspace)",
+                      (long long)n_pairs, num_experts, need, (size_t)QMOE_ROUTE_NOALLOC_SCRATCH_BYTES);
+  if (!offsets || !tile_row || !tile_exp || !ntiles || (max_tiles == 0 && n_pairs > 0))
+    return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (n_pairs > 0 && (!ids || !order || !inv_order || !sorted_ids)) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  hipStream_t st = qmoe::as_stream(stream);
+  int dev = -1, sdev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return qmoe::fail(QMOE_ERR_HIP, "hipGetDevice failed");
+  if (hipStreamGetDevice(st, &sdev) != hipSuccess) return qmoe::fail(QMOE_ERR_HIP, "hipStreamGetDevice failed");
+  if (sdev != dev)
+    return qmoe::fail(QMOE_ERR_INVALID, "stream is on device %d but device %d is current", sdev, dev);
+  int32_t* ws = nullptr;
+  const int rc = scratch_for_device(dev, &ws);
+  if (rc) return rc;
+  return route_launch(ids, n_pairs, num_experts, tile_rows, order, inv_order, sorted_ids, offsets, tile_row,
+                      tile_exp, ntiles, max_tiles, ws, n_bad ? n_bad : ws, st);
 }
