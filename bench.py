@@ -51,6 +51,8 @@ def parse():
                     help="run one workload's timed loop only, or 'copy' for the calibration copy kernel")
     ap.add_argument("--eager", action="store_true", help="launch the timed steps eagerly (no graph)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak probes")
+    ap.add_argument("--decode-phases", action="store_true",
+                    help="per-phase timestamps of the decode gate_up kernel (workload 1) from libqmoe_stamps.so")
     ap.add_argument("--traffic", action="store_true",
                     help="measure the decode kernel's HBM traffic live with rocprofv3 counter passes")
     return ap.parse_args()
@@ -760,6 +762,84 @@ def run_block(args, dev):
 SETUPS = {0: setup_cfg0, 1: setup_cfg1, 2: setup_cfg2, 3: setup_cfg3, 4: setup_cfg4, 5: setup_cfg5}
 
 
+def decode_phases(args, dev, samples=16):
+    """Workload 1 through the measurement build libqmoe_stamps.so, whose decode
+    GEMV writes s_memrealtime stamps (10 ns ticks) per block: entry, kernel
+    arguments ready, expert id ready, first weight row consumed, all rows
+    consumed and reduced, output store acknowledged.  The cycle is replayed
+    as time_graph does; after each of `samples` window replays the stamps of
+    that window's last launch are read.  Returns percentiles per phase (us)."""
+    import ctypes
+
+    import torch
+    from titan_amd import _lib, build as tbuild, synth
+
+    base = _lib.load()
+    L = ctypes.CDLL(str(tbuild.STAMPS_LIB))
+    fn = L.qmoe_moe_gate_up_swiglu
+    fn.restype, fn.argtypes = ctypes.c_int, base.qmoe_moe_gate_up_swiglu.argtypes
+    rd = L.qmoe_qmv_stamps_read
+    rd.restype, rd.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64]
+    wl, cycle, meta = setup_cfg1(args, dev)
+    # the same launches (weights, ids, outputs) through the stamped library
+    x = to_dev(wl["x"], "bf16", dev)
+    sets = weight_sets(wl, meta["sets"], dev, 101)
+    rng = np.random.default_rng(1001)
+    idxs = [torch.from_numpy(rng.permutation(256)[:10].astype(np.int32)[None]).to(dev) for _ in cycle]
+    out = torch.empty(1, 10, 512, dtype=torch.bfloat16, device=dev)
+
+    def mk(i):
+        w, s_, b = sets[i % len(sets)]
+        ix = idxs[i]
+
+        def f():
+            rc = fn(x.data_ptr(), ix.data_ptr(), 1, 10, 2048, w.data_ptr(), s_.data_ptr(), b.data_ptr(), 256, 512,
+                    64, 4, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"stamped qmoe_moe_gate_up_swiglu failed ({rc})")
+        return f
+
+    stamped = [mk(i) for i in range(len(cycle))]
+    sec, tinfo = time_graph(stamped, args.steps, args.warmup, dev)
+    sec_prod, _ = time_graph(cycle, args.steps, args.warmup, dev)
+    nb = 1280  # blocks of one launch: 10 experts x 512 gate/up row pairs / 4
+    names = ["entry", "args", "id", "first_row", "reduced", "stored"]
+    buf = np.zeros(nb * len(names), np.uint64)
+    rows = []
+    graphs = tinfo["graphs"]
+    for k in range(samples):
+        graphs[k % len(graphs)].replay()
+        torch.cuda.synchronize()
+        if rd(buf.ctypes.data, buf.size) != 0:
+            raise RuntimeError("qmoe_qmv_stamps_read failed")
+        rows.append(buf.reshape(nb, len(names)).astype(np.int64).copy())
+    tick_us = 0.01  # s_memrealtime runs at 100 MHz
+    pct = (0, 10, 50, 90, 100)
+
+    def q(v):
+        return [round(float(a), 3) for a in np.percentile(np.concatenate(v), pct)]
+
+    t0 = [r[:, 0] - r[:, 0].min() for r in rows]
+    res = {
+        "percentiles": list(pct),
+        "launch_offset_us": q([v * tick_us for v in t0]),
+        "args_wait_us": q([(r[:, 1] - r[:, 0]) * tick_us for r in rows]),
+        "id_wait_us": q([(r[:, 2] - r[:, 1]) * tick_us for r in rows]),
+        "first_weight_row_us": q([(r[:, 3] - r[:, 2]) * tick_us for r in rows]),
+        "other_rows_and_reduce_us": q([(r[:, 4] - r[:, 3]) * tick_us for r in rows]),
+        "store_ack_us": q([(r[:, 5] - r[:, 4]) * tick_us for r in rows]),
+        "block_end_offset_us": q([(r[:, 5] - r[:, 0].min()) * tick_us for r in rows]),
+        "dispatch_span_us": q([np.array([(r[:, 5].max() - r[:, 0].min()) * tick_us]) for r in rows]),
+        "stamped_us_per_call": round(sec * 1e6, 3),
+        "product_us_per_call": round(sec_prod * 1e6, 3),
+        "samples": samples,
+        "workload": meta["workload"],
+        "note": "stamps in 10 ns ticks; the stamped build loads the expert id through the vector path "
+                "(the timer intrinsic keeps the compiler from proving the id load scalar-safe)",
+    }
+    return res
+
+
 # ------------------------------------------------------------- CPU baseline
 
 
@@ -869,6 +949,9 @@ def main():
         return 0
     if args.only is not None:
         cfgs = [int(args.only)]
+    if args.decode_phases:
+        print(json.dumps({"decode_phases": decode_phases(args, dev)}))
+        return 0
     peaks = None
     if args.only is None and not args.no_peaks:
         print("[bench] measured peaks", file=sys.stderr, flush=True)

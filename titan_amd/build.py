@@ -3,8 +3,11 @@
 Each ``csrc/*.hip`` file is compiled to an object in parallel, then linked into
 ``titan_amd/lib/libqmoe.so``; ``csrc/peaks/peaks.hip`` (the bench's
 measured-ceiling probes, include/qmoe_peaks.h) becomes
-``titan_amd/lib/libqmoe_peaks.so``.  The libraries land in-tree so that they
-travel with the source tree; nothing is installed anywhere else.
+``titan_amd/lib/libqmoe_peaks.so``; and ``titan_amd/lib/libqmoe_stamps.so`` is
+libqmoe.so with the decode GEMV's per-phase timestamps compiled in
+(QMOE_QMV_STAMPS, read by ``bench.py --decode-phases``), a measurement build
+that nothing else loads.  The libraries land in-tree so that they travel with
+the source tree; nothing is installed anywhere else.
 
     python -m titan_amd.build            # build (always recompiles)
 """
@@ -27,6 +30,7 @@ LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libqmoe.so"
 PEAKS_SRC = CSRC / "peaks" / "peaks.hip"
 PEAKS_LIB = LIB_DIR / "libqmoe_peaks.so"
+STAMPS_LIB = LIB_DIR / "libqmoe_stamps.so"
 ARCH = os.environ.get("QMOE_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
@@ -49,10 +53,10 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libqmoe.so)")
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o",
-           str(obj)]
+def _compile(src: Path, variant: str = "", defines=()) -> Path:
+    obj = BUILD / (src.stem + variant + ".o")
+    cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), *(f"-D{d}" for d in defines), f"-I{INCLUDE}",
+           f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stdout}\n{r.stderr}")
@@ -75,12 +79,14 @@ def build(verbose: bool = False) -> Path:
     jobs = min(len(sources) + 1, max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
         fut_peaks = ex.submit(_compile, PEAKS_SRC)
+        fut_stamps = ex.submit(_compile, CSRC / "qmv.hip", "_stamps", ("QMOE_QMV_STAMPS",))
         objs = list(ex.map(_compile, sources))
-        peaks_obj = fut_peaks.result()
+        peaks_obj, stamps_obj = fut_peaks.result(), fut_stamps.result()
     _link(objs, LIB)
     _link([peaks_obj], PEAKS_LIB)
+    _link([o if o.stem != "qmv" else stamps_obj for o in objs], STAMPS_LIB)
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources and {PEAKS_LIB}")
+        print(f"built {LIB} from {len(sources)} sources, {PEAKS_LIB} and {STAMPS_LIB}")
     return LIB
 
 

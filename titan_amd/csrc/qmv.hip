@@ -311,8 +311,32 @@ __device__ __forceinline__ uint4 load_nt(const uint4* p) {
 // trips (kernel arguments, the expert id, the weights), so the expert id is
 // requested first, x next (it does not wait for the id), then the scales and
 // biases and the codes row by row, in the order they are consumed.
+#ifdef QMOE_QMV_STAMPS
+// Measurement build only (libqmoe_stamps.so, never the product library):
+// s_memrealtime stamps (100 MHz) of every block of qmv64_kernel, lane 0,
+// kStampsPerBlock per block -- entry, kernel arguments ready, expert id ready,
+// first weight row consumed, every weight row consumed and reduced, output
+// store acknowledged.  A launch overwrites the stamps of its blocks.
+constexpr int kStampsPerBlock = 6;
+constexpr int kStampBlocks = 16384;
+}  // namespace
+__device__ uint64_t qmv_stamps[kStampBlocks * kStampsPerBlock];
+namespace {
+// A stamp is ordered after the value it names has arrived (an empty asm that
+// reads the register makes the compiler wait for it there), so the stamped
+// kernel keeps the product kernel's load order.
+#define QMV_STAMP(var) const uint64_t var = __builtin_amdgcn_s_memrealtime()
+#define QMV_AFTER_S(v) asm volatile("" ::"s"(v))
+#define QMV_AFTER(v) asm volatile("" ::"v"(v))
+#else
+#define QMV_STAMP(var)
+#define QMV_AFTER_S(v)
+#define QMV_AFTER(v)
+#endif
+
 template <int NV, int TL, int MODE, int RG, int GS, bool GATHER, bool XROWS>
 __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
+  QMV_STAMP(ts_entry);
   // K = 2048 * NV + 512 * TL: NV whole chunks of 64 lanes x 32 elements and,
   // when TL > 0, a tail chunk held by lanes < 16 * TL (the others load
   // nothing and contribute zero: x = 0 there)
@@ -329,6 +353,8 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   const uint32_t bid = blockIdx.x;
   const uint32_t r = fast_div(bid, a.blk_div);
   const int n0 = (int)(bid - r * a.blk_div.d) * OUTS;
+  QMV_AFTER_S(r);
+  QMV_STAMP(ts_args);
   int e = GATHER ? a.experts[r] : 0;
   const uint32_t xr = XROWS ? (uint32_t)a.x_rows[r] : fast_div(r, a.x_divf);
   const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
@@ -342,6 +368,8 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
                                        : make_uint4(0u, 0u, 0u, 0u);
 
   e = min(max(e, 0), a.num_experts - 1);
+  QMV_AFTER_S(e);
+  QMV_STAMP(ts_id);
   constexpr int64_t KW = KE / 8;
   const int64_t ebase = (int64_t)e * a.n_w;
   const int grp1 = MODE == 1 ? a.n_out + n0 : n0 + RG;
@@ -399,6 +427,9 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   float part[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) part[q] = 0.f;
+#ifdef QMOE_QMV_STAMPS
+  uint64_t ts_first = 0;
+#endif
 #pragma unroll
   for (int g = 0; g < 2; ++g)
 #pragma unroll
@@ -412,8 +443,17 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
         acc += affine_chunk(dot_chunk(wv[g][i][v], xc[v], mv), xc[v].sum, sv, bv);
       }
       part[4 * g + i] = acc;
+#ifdef QMOE_QMV_STAMPS
+      if (g == 0 && i == 0) {
+        QMV_AFTER(acc);
+        QMV_STAMP(ts_first_);
+        ts_first = ts_first_;
+      }
+#endif
     }
   const float t = reduce8(part, lane);  // lanes 8q..: slot q
+  QMV_AFTER(t);
+  QMV_STAMP(ts_reduced);
   const int q = lane >> 3;
   if (MODE == 1) {
     // gate slot q (< 4) in lanes 8q, its up slot 4 + q in lanes 8q + 32
@@ -429,6 +469,14 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
       else a.out[(int64_t)r * a.n_out + n] = (uint16_t)f32_to_bf16(t);
     }
   }
+#ifdef QMOE_QMV_STAMPS
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  QMV_STAMP(ts_stored);
+  if (lane == 0 && bid < kStampBlocks) {
+    uint64_t* o = qmv_stamps + (size_t)bid * kStampsPerBlock;
+    o[0] = ts_entry; o[1] = ts_args; o[2] = ts_id; o[3] = ts_first; o[4] = ts_reduced; o[5] = ts_stored;
+  }
+#endif
 }
 
 // qmv64 over tile-layout weights (group 64): the code chunk of row n for
@@ -935,3 +983,15 @@ extern "C" int qmoe_moe_gate_up_swiglu_tiles(const uint16_t* x, const int32_t* i
             (int)(2 * I), h, sb};
   return launch_qmv_tiled<1>(a, qmoe::as_stream(stream));
 }
+
+#ifdef QMOE_QMV_STAMPS
+// Measurement build only: copies the first n stamps of qmv64_kernel's blocks
+// to host memory (after the stream has finished).
+extern "C" int qmoe_qmv_stamps_read(uint64_t* host, int64_t n) {
+  if (!host || n < 0 || n > (int64_t)kStampBlocks * kStampsPerBlock)
+    return qmoe::fail(QMOE_ERR_INVALID, "bad stamp count");
+  const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(qmv_stamps), (size_t)n * sizeof(uint64_t), 0,
+                                           hipMemcpyDeviceToHost);
+  return e == hipSuccess ? QMOE_OK : qmoe::fail(QMOE_ERR_HIP, "hipMemcpyFromSymbol: %s", hipGetErrorString(e));
+}
+#endif
