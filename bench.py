@@ -387,8 +387,8 @@ def setup_cfg1(args, dev):
         cursor[si] += 10
     idxs[0] = to_dev(wl["idx"], "i32", dev)
     outs = [torch.empty(1, 10, 512, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-    # load-time repack into the tile layout (outside the timed region)
-    tsets = [ops.repack_tiles(w, s, b) for (w, s, b) in sets]
+    # load-time repack into the gate/up-paired tile layout (outside the timed region)
+    tsets = [ops.repack_tiles(w, s, b, swiglu_pairs=True) for (w, s, b) in sets]
     torch.cuda.synchronize()
 
     def mk_tiles(i):
@@ -477,6 +477,8 @@ def setup_cfg2(args, dev):
     idxs = [idx] + [torch.from_numpy(a).to(dev) for a in idx_np[1:]]
     distinct = [int(np.unique(a).size) for a in idx_np]
     y = torch.empty(8, 2048, dtype=torch.bfloat16, device=dev)
+    tsets = [ops.repack_tiles(w, s, b) for (w, s, b) in sets]
+    torch.cuda.synchronize()
 
     def mk(i):
         w, s, b = sets[i % len(sets)]
@@ -488,13 +490,23 @@ def setup_cfg2(args, dev):
                           torch.cuda.current_stream().cuda_stream)
         return f
 
+    def mk_tiles(i):
+        tw = tsets[i % len(tsets)]
+        ii = idxs[i]
+
+        def f():
+            ops._lib.call("qmoe_moe_down_wsum_tiles", h.data_ptr(), ii.data_ptr(), sc.data_ptr(), 8, 10, 512,
+                          tw.wp.data_ptr(), tw.sb.data_ptr(), 256, 2048, y.data_ptr(),
+                          torch.cuda.current_stream().cuda_stream)
+        return f
+
     mean_distinct = float(np.mean(distinct))
     row_bytes = 512 // 2 + 8 * 4
     bytes_ = int(mean_distinct * 2048 * row_bytes + 8 * 10 * 512 * 2 + 8 * 2048 * 2 + 8 * 10 * 4)
     return wl, [mk(i) for i in range(L)], {
         "bytes": bytes_, "flops": synth.algorithmic_flops(2, wl), "bound": "hbm",
         "kernel": "down_pair_kernel<16>", "sets": len(sets), "mean_distinct_experts": mean_distinct,
-        "cycle_bytes": L * bytes_,
+        "cycle_bytes": L * bytes_, "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(L)]),
         "workload": "decode down + top-10 weighted sum: 8 tokens, I=512, D=2048, E=256, "
                     "W [256,2048,512] int4 g64 -> y [8,2048]"}
 
@@ -721,13 +733,13 @@ def run_block(args, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(107)
 
-    def block():
+    def block(resident="tiles"):
         gu = (random_like_words((256, 1024, 256), dev, gen), random_scales((256, 1024, 32), dev, gen),
               random_biases((256, 1024, 32), dev, gen))
         dn = (random_like_words((256, 2048, 64), dev, gen), random_scales((256, 2048, 8), dev, gen),
               random_biases((256, 2048, 8), dev, gen))
         router = (torch.randn(256, 2048, device=dev, generator=gen) * 0.05).to(torch.bfloat16)
-        return moe_block.SparseMoeBlock(router, gu, dn, 10)
+        return moe_block.SparseMoeBlock(router, gu, dn, 10, resident=resident)
 
     rng = np.random.default_rng(1007)
     res = {}
@@ -751,10 +763,19 @@ def run_block(args, dev):
             r.update(metric="TFLOP/s", value=round(fl / sec / 1e12, 1), flops_per_call=fl,
                      pct_bf16_peak=round(100 * fl / sec / 1e12 / BF16_PEAK_TFLOPS, 2),
                      path="router + top-k + route + SwiGLU GEMM + down GEMM + weighted sum")
+        r["resident"] = "tiles (one copy)"
         res[T] = r
         print(f"[bench] block T={T}: {r}", file=sys.stderr, flush=True)
         del blocks, fns, tinfo
         torch.cuda.empty_cache()
+        if T == 1:
+            # the same decode with the MLX tensors kept too (resident="both")
+            blocks = [block("both") for _ in range(nblocks)]
+            fns = [(lambda b=blocks[i % nblocks]: b(x)) for i in range(L)]
+            sec_b, _ = timer(args)(fns, steps, args.warmup, dev)
+            res[T]["us_per_call_resident_both"] = round(sec_b * 1e6, 3)
+            del blocks, fns
+            torch.cuda.empty_cache()
     return {"workload": "whole MoE block, E=256, H=2048, I=512, top-10, int4 g64 (tile layout for prefill)",
             "tokens": res}
 

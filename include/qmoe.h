@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 2
+#define QMOE_ABI_VERSION 3
 
 enum {
   QMOE_OK = 0,
@@ -226,21 +226,36 @@ int qmoe_gather_qmm_sorted_tiles(const uint16_t* x, const int32_t* x_rows,
                                  const int32_t* ntiles, int64_t max_tiles,
                                  uint16_t* out, void* stream);
 
-/* Decode gather-GEMV (qmoe_gather_qmv) and the fused gate_up + SwiGLU
- * (qmoe_moe_gate_up_swiglu) over tile-layout weights; same results as the
- * MLX-layout calls (the same factored arithmetic and reduction order), with
- * the scale|bias words of four rows read in one 16-byte load.  Requires
- * K = 2048*n (n <= 4) and 64 | rows per expert; I % 4 == 0 for the SwiGLU form. */
+/* Decode gather-GEMV (qmoe_gather_qmv) over tile-layout weights; same results
+ * as the MLX-layout call (the same factored arithmetic and reduction order).
+ * Requires K = 2048*n (n <= 4) and 64 | N. */
 int qmoe_gather_qmv_tiles(const uint16_t* x, const int32_t* x_rows,
                           const int32_t* experts, int64_t n_rows, int64_t K,
                           const uint32_t* wp, const uint32_t* sb,
                           int32_t num_experts, int64_t N, uint16_t* out,
                           void* stream);
+
+/* The fused decode gate_up + SwiGLU (qmoe_moe_gate_up_swiglu) over tile-layout
+ * weights in the gate/up-PAIRED row order of
+ * qmoe_gather_qmm_swiglu_sorted_tiles (one resident copy serves both the
+ * decode and the prefill gate_up): the MLX-layout call's arithmetic per
+ * 32-code chunk, summed in another order.  Requires K = 2048*n (n <= 4) and
+ * 32 | I. */
 int qmoe_moe_gate_up_swiglu_tiles(const uint16_t* x, const int32_t* idx,
                                   int64_t T, int64_t top_k, int64_t K,
                                   const uint32_t* wp, const uint32_t* sb,
                                   int32_t num_experts, int64_t I, uint16_t* h,
                                   void* stream);
+
+/* The fused decode down + weighted sum (qmoe_moe_down_wsum, replacing
+ * engine/patches/decode-fusion/fused_kernels.py:93-169,213-231) over
+ * tile-layout down weights [E, D, I]; bit-identical to the MLX-layout call.
+ * Requires I = 512, 64 | D, T <= 16, top_k <= 16. */
+int qmoe_moe_down_wsum_tiles(const uint16_t* h, const int32_t* idx,
+                             const float* scores, int64_t T, int64_t top_k,
+                             int64_t I, const uint32_t* wp, const uint32_t* sb,
+                             int32_t num_experts, int64_t D, uint16_t* y,
+                             void* stream);
 
 /* ------------------------------------------------------------------ int8 --
  * int8-activation x int4-weight gate_up (replaces

@@ -105,3 +105,65 @@ def test_patched_switchglu_matches_the_oracle_chain(dev, orc, T):
     else:
         # unsorted: both projections through the decode overlay's gather-GEMV
         assert routed == 2 and "moe_gather_ws.calls" not in reg.counters()
+
+
+def test_warmup_prepares_tile_layouts_and_the_overlays_run_on_them(dev, orc, monkeypatch):
+    """warmup(model) repacks each routed weight tensor into the tile layout once
+    (engine/patches/moe-int8/patch.py:179-198); the prefill calls after it read
+    those copies -- the bf16 registry path and the int8 overlay share them --
+    and match the oracle."""
+    from titan_amd import kernels
+    from titan_amd.kernels import prepared
+    from titan_amd.patches import gather_ws, moe_int8
+
+    say("warmup + tile-layout prefill through the registry and the int8 overlay")
+    rng = np.random.default_rng(77)
+    E, K, I, k, T = 16, 512, 512, 10, 16
+    gu, dn = _quant(rng, E, 2 * I, K), _quant(rng, E, K, I)
+    x16 = synth.bf16_bits(rng.normal(size=(T, K)).astype(np.float32))
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    lin = lambda t: QuantizedSwitchLinear(words_t(t[0], dev), bf16_t(t[1], dev), bf16_t(t[2], dev))
+    glu = SwitchGLU(lin(dn), gate_up_proj=lin(gu))
+    model = {"layers": [{"mlp": glu}]}
+    prepared.clear_cache()
+    assert gather_ws.warmup(model) == 2
+    st0 = prepared.stats()
+    assert st0["built"] >= 2 and st0["entries"] == 2
+    kernels.reset()
+    R.build_registry(R.KernelConfig(fail_open=False))
+    try:
+        y = glu(bf16_t(x16, dev), i32_t(ids, dev))
+        torch.cuda.synchronize()
+    finally:
+        kernels.reset()
+    st1 = prepared.stats()
+    assert st1["hits"] - st0["hits"] == 2 and st1["built"] == st0["built"]  # both projections, no rebuild
+    ref = _oracle_chain(orc, x16, ids, gu, dn)
+    err = np.abs(orc.f32_from_bf16(bits(y)).astype(np.float64) - ref).max()
+    assert err <= 2.0 ** -7 * np.abs(ref).max()
+
+    # the int8 overlay: its tables are the same prepared copies
+    monkeypatch.setenv("TITAN_AMD_MOE_INT8_PREFILL", "1")
+    monkeypatch.setenv("TITAN_AMD_MOE_INT8_MIN_ROWS", "64")
+    assert moe_int8.warmup(model) == 2
+    assert prepared.stats()["built"] == st1["built"]
+    from titan_amd.kernels import moe_gather_int8
+
+    tabs = moe_gather_int8.build_tables(glu.gate_up_proj.weight, glu.gate_up_proj.scales, glu.gate_up_proj.biases)
+    assert tabs.nbytes == sum(a.nbytes for a in gu)
+    ns = type("NS", (), {"gather_qmm": staticmethod(stock.gather_qmm),
+                         "quantized_matmul": staticmethod(stock.quantized_matmul)})
+    srt = np.sort(ids.reshape(-1)).astype(np.int32)
+    xs = synth.bf16_bits(rng.normal(size=(srt.size, K)).astype(np.float32))
+    assert moe_int8.install(ns) is True
+    try:
+        r0 = moe_int8.stats()["routed"]
+        out = ns.gather_qmm(bf16_t(xs, dev).reshape(-1, 1, K), glu.gate_up_proj.weight, glu.gate_up_proj.scales,
+                            glu.gate_up_proj.biases, rhs_indices=i32_t(srt, dev), sorted_indices=True)
+        torch.cuda.synchronize()
+        assert moe_int8.stats()["routed"] - r0 == 1
+    finally:
+        moe_int8.uninstall()
+    rxi, rsx = orc.quant_act_int8(xs)
+    ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, None, srt, *gu)
+    assert_close_bf16(orc, bits(out).reshape(srt.size, -1), ref64, what="int8 overlay on prepared tiles")

@@ -154,14 +154,16 @@ def test_moe_block_matches_oracle_chain(dev, orc, T, smp):
     if T * k < blk.sort_min_pairs and T <= 16:
         # stage 2: h = silu(gate) * up per (token, slot); stage 3: the fused
         # down + weighted sum, the oracle fed the kernel's own h
-        h = ops.gate_up_silu(xt, *blk.gate_up, idx)
+        # the block keeps one resident copy, in the tile layout, and decodes from it
+        assert blk.decode_tiles and blk.gate_up is None and blk.down is None
+        h = ops.gate_up_silu_tiles(xt, blk.gu_tiles, idx)
         tok = np.repeat(np.arange(T), k).astype(np.int32)
         gu64, _ = orc.gather_qmm_rows(x, tok, ridx.reshape(-1), *gu)
         h64, _ = orc.swiglu(gu64)
         assert_close_bf16(orc, bits(h).reshape(T * k, I), h64, what=f"block h T={T}")
         y64, _ = orc.down_wsum(bits(h), ridx, sc32, *dn)
         assert_close_bf16(orc, y, y64, what=f"block y T={T}")
-        want = bits(ops.down_wsum(h, *blk.down, idx, sc))
+        want = bits(ops.down_wsum_tiles(h, blk.down_tiles, idx, sc))
     else:
         # stage 2: routing sort + SwiGLU gate_up GEMM; stage 3: down GEMM on
         # the kernel's own h; stage 4: un-permute + weighted sum, bit-exact
@@ -204,3 +206,32 @@ def test_moe_block_shared_expert(dev, orc, T):
     err = np.abs(y - want).max() / np.abs(want).max()
     print(f"[parity] shared block rel_to_max {err:.3g}", flush=True)
     assert err <= 2.0 ** -7
+
+
+@pytest.mark.parametrize("resident", ["tiles", "both"])
+def test_moe_block_resident_copies(dev, orc, resident):
+    """resident="tiles": one tile-layout copy, the same bytes as the MLX tensors
+    it was built from (the layout is a permutation); "both": twice that.  The
+    two blocks' decode outputs both meet the oracle's bar."""
+    E, H, I, k, T = 16, 2048, 512, 4, 2
+    say(f"MoE block resident={resident}")
+    gu, dn, router, (sgu, sdn, sg) = _block_problem(3, E, H, I, with_shared=True)
+    shared = moe_block.SharedExpert(_dev_w(sgu, dev), _dev_w(sdn, dev), bf16_t(sg, dev))
+    blk = moe_block.SparseMoeBlock(bf16_t(router, dev), _dev_w(gu, dev), _dev_w(dn, dev), k, shared=shared,
+                                   resident=resident)
+    mlx_bytes = sum(a.nbytes for grp in (gu, dn, sgu, sdn) for a in grp)
+    assert blk.nbytes == (1 if resident == "tiles" else 2) * mlx_bytes, (blk.nbytes, mlx_bytes)
+    assert blk.decode_tiles == (resident == "tiles")
+    rng = np.random.default_rng(5)
+    x = synth.bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
+    xt = bf16_t(x, dev)
+    idx, sc = blk.route(xt)
+    y = bits(blk.experts(xt, idx, sc))
+    ridx = idx.cpu().numpy()
+    tok = np.repeat(np.arange(T), k).astype(np.int32)
+    gu64, _ = orc.gather_qmm_rows(x, tok, ridx.reshape(-1), *gu)
+    _, h16 = orc.swiglu(gu64)
+    y64, _ = orc.down_wsum(h16.reshape(T, k, I), ridx, sc.cpu().numpy(), *dn)
+    rep = orc.err_report(y, y64)
+    print(f"[parity] block resident={resident}: {rep}", flush=True)
+    assert rep["rel_to_max"] <= 2.0 ** -7

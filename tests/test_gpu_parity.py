@@ -473,30 +473,30 @@ def test_gate_up_swiglu_tiles_cfg1_matches_mlx_layout(dev, orc):
     say("gate_up + SwiGLU tile layout, workload 1")
     wl = synth.make(1)
     w, s, b = words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev)
-    tw = ops.repack_tiles(w, s, b)
+    tw = ops.repack_tiles(w, s, b, swiglu_pairs=True)
     idx = i32_t(wl["idx"], dev)
     h_t = ops.gate_up_silu_tiles(bf16_t(wl["x"], dev), tw, idx)
-    h_m = ops.gate_up_silu(bf16_t(wl["x"], dev), w, s, b, idx)
-    assert np.array_equal(bits(h_t), bits(h_m))
     gu64, _ = orc.gather_qmm_rows(wl["x"], np.zeros(10, np.int32), wl["idx"].reshape(-1), wl["w"],
                                   wl["s"], wl["b"])
     h64, _ = orc.swiglu(gu64)
     assert_close_bf16(orc, bits(h_t).reshape(10, 512), h64, what="cfg1 swiglu tiles")
 
 
-@pytest.mark.parametrize("T,k,E,I,K", [(3, 4, 16, 96, 2048), (1, 10, 16, 256, 4096), (2, 2, 4, 64, 6144)])
+@pytest.mark.parametrize("T,k,E,I,K", [(3, 4, 16, 96, 2048), (1, 10, 16, 256, 4096), (2, 2, 4, 64, 6144),
+                                       (2, 3, 4, 32, 8192), (16, 10, 64, 512, 2048)])
 def test_gate_up_swiglu_tiles_shapes(dev, orc, T, k, E, I, K):
     say(f"gate_up tiles T={T} k={k} E={E} I={I} K={K}")
     rng = np.random.default_rng(T * 1000 + K)
     w, s, b = synth.quant_weights(rng, (E, 2 * I), K)
     x = synth.bf16_bits(rng.normal(size=(T, K)).astype(np.float32))
     idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
-    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), swiglu_pairs=True)
     h = ops.gate_up_silu_tiles(bf16_t(x, dev), tw, i32_t(idx, dev))
     rows = np.repeat(np.arange(T, dtype=np.int32), k)
     gu64, _ = orc.gather_qmm_rows(x, rows, idx.reshape(-1), w, s, b)
     h64, _ = orc.swiglu(gu64)
     assert_close_bf16(orc, bits(h).reshape(T * k, I), h64, what=f"gate_up tiles {T}/{k}/{E}/{I}/{K}")
+
 
 
 @pytest.mark.parametrize("R,E,N,K", [(1, 1, 4096, 2048), (7, 8, 192, 4096), (5, 3, 64, 8192)])
@@ -692,3 +692,24 @@ def test_fused_decode_group_sizes(dev, orc, gs):
                           f32_t(sc[:TT], dev), group_size=gs)
         y64, _ = orc.down_wsum(bits(h[:TT]), idx[:TT], sc[:TT], wd, sd, bd, group_size=gs)
         assert_close_bf16(orc, bits(y), y64, what=f"down gs{gs} T={TT}")
+
+
+@pytest.mark.parametrize("T,E,D", [(1, 256, 2048), (3, 64, 2048), (8, 256, 2048), (16, 32, 192)])
+def test_down_wsum_tiles_matches_mlx_layout(dev, orc, T, E, D):
+    """The fused down + weighted sum over tile-layout down weights: bit-identical
+    to the MLX-layout kernel (the same 32 codes per lane, the same reduction)
+    and within the bar of the oracle."""
+    say(f"down + weighted sum tiles T={T} E={E} D={D}")
+    wl = synth.make(2, seed=300 + T, tokens=T, experts=E)
+    if D != 2048:
+        rng = np.random.default_rng(D)
+        w, s_, b = synth.quant_weights(rng, (E, D), 512)
+    else:
+        w, s_, b = wl["w"], wl["s"], wl["b"]
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s_, dev), bf16_t(b, dev))
+    h, idx, sc = bf16_t(wl["h"], dev), i32_t(wl["idx"], dev), f32_t(wl["scores"], dev)
+    yt = ops.down_wsum_tiles(h, tw, idx, sc)
+    ym = ops.down_wsum(h, words_t(w, dev), bf16_t(s_, dev), bf16_t(b, dev), idx, sc)
+    assert torch.equal(yt, ym)
+    y64, _ = orc.down_wsum(wl["h"], wl["idx"], wl["scores"], w, s_, b)
+    assert_close_bf16(orc, bits(yt), y64, what=f"down tiles T={T}")

@@ -183,3 +183,29 @@ def test_stats_and_companions_exist():
         assert m.warmup() == 0
         m.clear_cache()
     assert set(patches.stats()) == {"gather_qmv", "gather_ws", "moe_int8"}
+
+
+def test_switch_linears_finds_nested_layers():
+    """warmup's walk: layers inside containers, attributes and named_modules."""
+    from titan_amd.patches._overlay import switch_linears
+    from titan_amd.switch_layers import QuantizedSwitchLinear, SwitchGLU
+
+    z = torch.zeros(2, 64, 32, dtype=torch.int32)
+    sc = torch.zeros(2, 64, 4, dtype=torch.bfloat16)
+    a, b, c = (QuantizedSwitchLinear(z, sc, sc) for _ in range(3))
+    glu = SwitchGLU(a, gate_up_proj=b)
+
+    class Mod:
+        def __init__(self, kids):
+            self.kids = kids
+
+        def named_modules(self):
+            yield "", self
+            for i, kd in enumerate(self.kids):
+                yield str(i), kd
+
+    model = {"blocks": [glu, Mod([c, glu])], "other": "x"}
+    found = switch_linears(model)
+    assert sorted(map(id, found)) == sorted(map(id, (a, b, c)))
+    # CPU tensors: nothing to prepare, the walk still completes
+    assert moe_int8.warmup(model) == 0 and gather_ws.warmup(model) == 0

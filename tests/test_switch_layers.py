@@ -93,3 +93,29 @@ def test_swiglu_is_silu_gate_times_up():
     u = torch.tensor([1.0, 3.0, -2.0]).to(torch.bfloat16)
     want = (g.float() * torch.sigmoid(g.float()) * u.float()).to(torch.bfloat16)
     assert torch.equal(swiglu(g, u), want)
+
+
+def test_custom_activation_gets_up_then_gate(orc):
+    """SwitchGLU calls activation(x_up, x_gate), as the reference does
+    (switch_layers.py:237, with SwiGLU.__call__(x, gate) at :189-194): an
+    asymmetric activation sees the up half first."""
+    from titan_amd.switch_layers import SwiGLU
+
+    rng = np.random.default_rng(3)
+    E, K, I, k = 4, 128, 64, 2
+    gu, gu_layer = _layer(orc, rng, E, 2 * I, K)
+    dn, dn_layer = _layer(orc, rng, E, K, I)
+    x = bf16_t(orc.bf16_from_f32(rng.normal(size=(2, K)).astype(np.float32)))
+    ids = torch.tensor([[0, 1], [2, 3]])
+    seen = {}
+
+    def take_first(a, b):
+        seen["first"], seen["second"] = a, b
+        return a
+
+    SwitchGLU(dn_layer, gate_up_proj=gu_layer, activation=take_first)(x, ids)
+    up_then_gate = gu_layer(x.unsqueeze(-2).unsqueeze(-2), ids).chunk(2, dim=-1)
+    assert torch.equal(seen["first"], up_then_gate[1]) and torch.equal(seen["second"], up_then_gate[0])
+    # the default module computes silu(gate) * up from that order
+    g, u = up_then_gate[0], up_then_gate[1]
+    assert torch.equal(SwiGLU()(u, g), swiglu(g, u))

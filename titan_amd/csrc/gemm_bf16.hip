@@ -316,12 +316,13 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, char* smem, const 
     __syncthreads();
     constexpr int kIt = kPassRows * 32 / kThreads;
     i32x4_t v[kIt];
+    uint32_t ad[kIt];
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int m = it * (kThreads / 32) + tid / 32;
-      lds_read16(v[it], ep + m * 512 + (((tid % 32) ^ (m & 31)) * 16));
+      ad[it] = (uint32_t)(uintptr_t)(ep + m * 512 + (((tid % 32) ^ (m & 31)) * 16));
     }
-    lds_wait_all(v);
+    lds_read16_all(v, ad);
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int m = it * (kThreads / 32) + tid / 32;
@@ -376,12 +377,13 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, char* smem,
     __syncthreads();
     constexpr int kIt = kPassRows * 16 / kThreads;
     i32x4_t v[kIt];
+    uint32_t ad[kIt];
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int m = it * (kThreads / 16) + tid / 16;
-      lds_read16(v[it], ep + m * 256 + (((tid % 16) ^ (m & 15)) * 16));
+      ad[it] = (uint32_t)(uintptr_t)(ep + m * 256 + (((tid % 16) ^ (m & 15)) * 16));
     }
-    lds_wait_all(v);
+    lds_read16_all(v, ad);
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int m = it * (kThreads / 16) + tid / 16;

@@ -57,17 +57,42 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
 // 16-byte LDS reads whose results are only waited for together: an epilogue
 // reads all of a pass's staged row pieces, then stores them.  (Written as
 // plain loads, the compiler sinks each read next to its row-guarded store,
-// and every read's latency is exposed.)  The reads are asm, so the compiler
-// does not track them: lds_wait_all waits for them and passes the values on
-// through empty asm, which keeps every use after the wait.
-__device__ __forceinline__ void lds_read16(i32x4_t& v, const void* p) {
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"((uint32_t)(uintptr_t)p) : "memory");
+// and every read's latency is exposed.)  The reads and their
+// s_waitcnt lgkmcnt(0) are one asm statement, so no output register is read
+// or copied before the data has arrived; the outputs are early-clobber so no
+// address register of a later read shares a destination of an earlier one.
+// a[i] are LDS byte addresses.
+__device__ __forceinline__ void lds_read16x4(i32x4_t (&v)[4], const uint32_t (&a)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b128 %2, %6\n\t"
+      "ds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3])
+      : "memory");
+}
+__device__ __forceinline__ void lds_read16x8(i32x4_t (&v)[8], const uint32_t (&a)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %9\n\t"
+      "ds_read_b128 %2, %10\n\t"
+      "ds_read_b128 %3, %11\n\t"
+      "ds_read_b128 %4, %12\n\t"
+      "ds_read_b128 %5, %13\n\t"
+      "ds_read_b128 %6, %14\n\t"
+      "ds_read_b128 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+      : "memory");
 }
 template <int N>
-__device__ __forceinline__ void lds_wait_all(i32x4_t (&v)[N]) {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+__device__ __forceinline__ void lds_read16_all(i32x4_t (&v)[N], const uint32_t (&a)[N]) {
+  static_assert(N == 4 || N == 8, "4 or 8 reads");
+  if constexpr (N == 4) lds_read16x4(v, a);
+  else lds_read16x8(v, a);
 }
 
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;

@@ -479,22 +479,32 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
 #endif
 }
 
-// qmv64 over tile-layout weights (group 64): the code chunk of row n for
-// group g, half h is 16 bytes at ((((e*NC + n/64)*G + g)*2 + (n%64)/32)*2 + h)*32
-// + n%32, so the four consecutive rows a wave reads at one (g, h) form one
-// 64-byte segment; their scale|bias words are 16 contiguous bytes of the
-// group's 256-byte chunk.  Loads are issued in the order they are consumed
-// (x, scale|bias, then codes row by row) so the arithmetic starts as data
-// lands.  Rows n0..n0+OUTS-1 with n0 a multiple of 4.
-template <int NV, int MODE>
+// Block id -> work item, XCD-contiguous: the hardware deals consecutive block
+// ids round-robin to the 8 XCDs, so with nb % 8 == 0 item v = (b % 8) * nb/8
+// + b / 8 puts consecutive items -- row groups that share 128-byte code lines
+// or a 256-byte scale|bias chunk of the tile layout -- on one XCD, where the
+// second reader finds the line in that XCD's L2.  A permutation of [0, nb).
+__device__ __forceinline__ uint32_t xcd_item(uint32_t b, uint32_t nb) {
+  return (nb & 7u) ? b : (b & 7u) * (nb >> 3) + (b >> 3);
+}
+
+// qmv64 over tile-layout weights (group 64), plain row form: the code chunk of
+// row n for group g, half h is 16 bytes at
+// ((((e*NC + n/64)*G + g)*2 + (n%64)/32)*2 + h)*32 + n%32 (16-byte units), so
+// the eight consecutive rows n0.. (n0 % 8 == 0) a wave reads at one (g, h)
+// form one whole 128-byte line; their scale|bias words are 32 contiguous
+// bytes of the group's 256-byte chunk, which eight consecutive items share.
+// Loads are issued in the order they are consumed (x, scale|bias, then codes
+// row by row) so the arithmetic starts as data lands.
+template <int NV>
 __global__ __launch_bounds__(64) void qmv64_tiled_kernel(QmvArgs a) {
-  constexpr int OUTS = MODE == 1 ? 4 : 8;
-  constexpr int NQ = 8 / 4;  // 16-byte scale|bias loads per wave-slot of four rows
+  constexpr int OUTS = 8;
   const int lane = threadIdx.x;
+  const uint32_t item = xcd_item(blockIdx.x, gridDim.x);
   const int64_t nblk = (a.n_out + OUTS - 1) / OUTS;
-  const int64_t r = blockIdx.x / nblk;
+  const int64_t r = item / nblk;
   if (r >= a.n_pairs) return;
-  const int n0 = (int)(blockIdx.x % nblk) * OUTS;
+  const int n0 = (int)(item % nblk) * OUTS;
   int e = a.experts ? a.experts[r] : 0;
   e = min(max(e, 0), a.num_experts - 1);
   const int64_t xr = a.x_rows ? (int64_t)a.x_rows[r] : r / a.x_div;
@@ -507,25 +517,22 @@ __global__ __launch_bounds__(64) void qmv64_tiled_kernel(QmvArgs a) {
 #pragma unroll
   for (int v = 0; v < NV; ++v) load_x_chunk(xrow + v * 2048 + lane * 32, xc[v]);
 
-  // the two row quads: MODE 1 gate rows n0.. and up rows n_out + n0..; MODE 0 rows n0.. and n0 + 4..
-  int quad_row[NQ];
-  quad_row[0] = n0;
-  quad_row[1] = MODE == 1 ? a.n_out + n0 : n0 + 4;
-  uint4 sbv[NQ][NV];
+  // rows n0 .. n0 + 7 (clamped into the expert; n_w % 64 == 0 keeps a clamped
+  // row group inside one 32-row half)
+  const int nq = min(n0, a.n_w - 8);
+  uint4 sbv[2][NV];
 #pragma unroll
-  for (int u = 0; u < NQ; ++u) {
-    const int n = min(quad_row[u], a.n_w - 4);
+  for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int g = v * 32 + (lane >> 1);
-      const int64_t chunk = ((int64_t)e * NC + n / 64) * G + g;
-      sbv[u][v] = *reinterpret_cast<const uint4*>(a.sb + chunk * 64 + (n & 63));
+      const int64_t chunk = ((int64_t)e * NC + nq / 64) * G + g;
+      sbv[u][v] = *reinterpret_cast<const uint4*>(a.sb + chunk * 64 + (nq & 63) + 4 * u);
     }
-  }
   uint4 wv[8][NV];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
-    const int n = min(quad_row[q >> 2], a.n_w - 4) + (q & 3);
+    const int n = nq + q;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int g = v * 32 + (lane >> 1);
@@ -547,16 +554,226 @@ __global__ __launch_bounds__(64) void qmv64_tiled_kernel(QmvArgs a) {
     }
   }
   const float t = reduce8(part, lane);  // lanes 8q..: row q
-  if (MODE == 1) {
+  const int q = lane >> 3;
+  if ((lane & 7) == 0 && n0 + q < a.n_out) a.out[r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t);
+}
+
+// Fused gate_up + SwiGLU over tile-layout weights in the gate/up-PAIRED row
+// order of the SwiGLU grouped GEMM: the gate row of intermediate index i is
+// paired row 64(i/32) + i%32 and its up row sits 32 rows below, so in the tile
+// layout the two are halves j = 0 and 1 of one 64-row block, with the same row
+// l = i%32 in the half.  A wave computes RG consecutive indices i0.. (RG | 32):
+// per group g and half h its RG gate rows are RG*16 contiguous bytes of the
+// chunk and its up rows another RG*16 (RG = 8: one whole 128-byte line each),
+// and their scale|bias words RG*4 contiguous bytes each.  Items are dealt
+// XCD-contiguously (xcd_item), so the row groups sharing a scale|bias chunk
+// run on one XCD.  Per lane and row the arithmetic and the reduction tree are
+// those of qmv64_kernel's fused form, so the result is bit-identical to it.
+template <int NV, int RG>
+__global__ __launch_bounds__(64) void qmv64_paired_kernel(QmvArgs a) {
+  static_assert(RG == 4 || RG == 8, "four or eight indices per wave");
+  const int lane = threadIdx.x;
+  const uint32_t item = xcd_item(blockIdx.x, gridDim.x);
+  const uint32_t r = fast_div(item, a.blk_div);
+  const int i0 = (int)(item - r * a.blk_div.d) * RG;
+  int e = a.experts[r];
+  const uint32_t xr = fast_div(r, a.x_divf);
+  const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
+  uint4 xa[NV][4];
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q];
+  e = min(max(e, 0), a.num_experts - 1);
+  const int G = 32 * NV;
+  const int NC = a.n_w / 64;
+  const int c = i0 >> 5, l0 = i0 & 31;
+  const int h = lane & 1;
+  const int64_t chunk0 = ((int64_t)e * NC + c) * G + (lane >> 1);  // chunk of the lane's group in column block c
+
+  // scale|bias words: gate rows at l0.., up rows at 32 + l0.., RG/4 16-byte loads each
+  uint4 sg[NV][RG / 4], su[NV][RG / 4];
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int t = 0; t < RG / 4; ++t) {
+      const uint32_t* base = a.sb + (chunk0 + v * 32) * 64 + l0 + 4 * t;
+      sg[v][t] = *reinterpret_cast<const uint4*>(base);
+      su[v][t] = *reinterpret_cast<const uint4*>(base + 32);
+    }
+  uint4 wg[RG][NV], wu[RG][NV];
+#pragma unroll
+  for (int q = 0; q < RG; ++q)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const uint4* units = reinterpret_cast<const uint4*>(a.w) + ((chunk0 + v * 32) * 4 + h) * 32 + l0 + q;
+      wg[q][v] = load_nt(units);       // half j = 0: gate
+      wu[q][v] = load_nt(units + 64);  // half j = 1: up, two 32-unit halves further
+    }
+  XChunk xc[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 t = xa[v][q];
+      xc[v].p[4 * q + 0] = (t.x & 0xFFFFu) | (t.z << 16);
+      xc[v].p[4 * q + 1] = (t.x >> 16) | (t.z & 0xFFFF0000u);
+      xc[v].p[4 * q + 2] = (t.y & 0xFFFFu) | (t.w << 16);
+      xc[v].p[4 * q + 3] = (t.y >> 16) | (t.w & 0xFFFF0000u);
+      sum += ((bf16lo(t.x) + bf16hi(t.x)) + (bf16lo(t.y) + bf16hi(t.y))) +
+             ((bf16lo(t.z) + bf16hi(t.z)) + (bf16lo(t.w) + bf16hi(t.w)));
+    }
+    xc[v].sum = sum;
+  }
+  const uint32_t mv = magic_vgpr();
+  auto word_of = [](const uint4& u, int k) { return k == 0 ? u.x : k == 1 ? u.y : k == 2 ? u.z : u.w; };
+#pragma unroll
+  for (int b = 0; b < RG / 4; ++b) {
+    // slots 0..3: gate rows 4b.., 4..7: their up rows
+    float part[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float pg = 0.f, pu = 0.f;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const uint32_t wgs = word_of(sg[v][b], q), wus = word_of(su[v][b], q);
+        pg += affine_chunk(dot_chunk(wg[4 * b + q][v], xc[v], mv), xc[v].sum, __uint_as_float(wgs << 16),
+                           __uint_as_float(wgs & 0xFFFF0000u));
+        pu += affine_chunk(dot_chunk(wu[4 * b + q][v], xc[v], mv), xc[v].sum, __uint_as_float(wus << 16),
+                           __uint_as_float(wus & 0xFFFF0000u));
+      }
+      part[q] = pg;
+      part[4 + q] = pu;
+    }
+    const float t = reduce8(part, lane);  // lanes 8q..: slot q
+    // gate slot q (< 4) in lanes 8q, its up slot 4 + q in lanes 8q + 32
     auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
     const float up = as_f(sw[1]);
     const int q = lane >> 3;
-    if (lane < 32 && (lane & 7) == 0 && n0 + q < a.n_out)
-      a.out[r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t / (1.0f + expf(-t)) * up);
-  } else {
-    const int q = lane >> 3;
-    if ((lane & 7) == 0 && n0 + q < a.n_out) a.out[r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t);
+    if (lane < 32 && (lane & 7) == 0)
+      a.out[(int64_t)r * a.n_out + i0 + 4 * b + q] = (uint16_t)f32_to_bf16(t / (1.0f + expf(-t)) * up);
   }
+}
+
+// Fused gate_up + SwiGLU over the gate/up-paired tile layout with line reads:
+// a wave computes RG indices i0 .. (gate rows l0 .. l0 + RG - 1 of half j = 0
+// of column block c = i0 / 32, up rows in half j = 1).  Lane 8r + s holds row
+// slot r and group slot s; its load (p, h) reads the 16-byte unit
+// (g = 8p + s, j, h, l0 + rr) of its row, so the lanes of one group slot read
+// consecutive rows of one (g, j, h): RG = 8 gives each slot two whole 128-byte
+// lines (rows of gate and of up, r = 0..7 each), RG = 4 one 64-byte half-line
+// of gate rows (r < 4) and one of up rows (r >= 4), whose other halves the
+// XCD-adjacent item reads.  x changes with the group, so the wave stages its x
+// row in LDS once (per 32-element chunk: the 16 bf16 pairs matched to the
+// nibble pairs, and the chunk's sum) and each lane reads the chunk of its
+// (g, h) per step.  Per lane the affine chunk arithmetic is qmv64_kernel's;
+// the row sums close over the eight group slots with three DPP steps.
+template <int NV, int RG>
+__global__ __launch_bounds__(64) void qmv64_paired_lines_kernel(QmvArgs a) {
+  static_assert(RG == 4 || RG == 8, "four or eight indices per wave");
+  constexpr int NCH = 64 * NV;   // 32-element chunks of x
+  constexpr int NP = 4 * NV;     // group steps per lane: g = 8p + s
+  constexpr int NJ = RG / 4;     // row halves a lane reads: both (RG = 8) or its own (RG = 4)
+  __shared__ uint4 xl[4][NCH];   // quarter q of chunk c at xl[q][c]: 16-byte reads of 8 chunks hit distinct banks
+  __shared__ float xsum[NCH];
+  const int lane = threadIdx.x;
+  const int r = lane >> 3, sl = lane & 7;
+  const int jr = RG == 8 ? 0 : r >> 2;        // RG = 4: the lane's half (gate or up)
+  const int rr = RG == 8 ? r : (r & 3);       // row within the wave's RG rows
+  const uint32_t item = xcd_item(blockIdx.x, gridDim.x);
+  const uint32_t pr = fast_div(item, a.blk_div);
+  const int i0 = (int)(item - pr * a.blk_div.d) * RG;
+  int e = a.experts[pr];
+  const uint32_t xr = fast_div(pr, a.x_divf);
+  const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
+  uint4 xa[NV][4];
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q];
+  e = min(max(e, 0), a.num_experts - 1);
+  const int G = 32 * NV;
+  const int NC = a.n_w / 64;
+  const int c = i0 >> 5, l0 = i0 & 31;
+  const int64_t cbase = ((int64_t)e * NC + c) * G;  // chunk of group 0 in column block c
+
+  uint32_t sbw[NP][NJ];
+  uint4 wv[NP][2][NJ];  // [step][h][row half]
+#pragma unroll
+  for (int pp = 0; pp < NP; ++pp) {
+    const uint32_t* sbc = a.sb + (cbase + 8 * pp + sl) * 64 + l0 + rr;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) sbw[pp][jj] = sbc[32 * (jr + jj)];
+  }
+#pragma unroll
+  for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj) {
+        const int64_t chunk = cbase + 8 * pp + sl;
+        wv[pp][h][jj] = load_nt(reinterpret_cast<const uint4*>(a.w) + ((chunk * 2 + jr + jj) * 2 + h) * 32 + l0 + rr);
+      }
+  // stage x: lane l writes chunk v*64 + l (elements v*2048 + 32l ..)
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    uint32_t pw[16];
+    float sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 t = xa[v][q];
+      pw[4 * q + 0] = (t.x & 0xFFFFu) | (t.z << 16);
+      pw[4 * q + 1] = (t.x >> 16) | (t.z & 0xFFFF0000u);
+      pw[4 * q + 2] = (t.y & 0xFFFFu) | (t.w << 16);
+      pw[4 * q + 3] = (t.y >> 16) | (t.w & 0xFFFF0000u);
+      sum += ((bf16lo(t.x) + bf16hi(t.x)) + (bf16lo(t.y) + bf16hi(t.y))) +
+             ((bf16lo(t.z) + bf16hi(t.z)) + (bf16lo(t.w) + bf16hi(t.w)));
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xl[q][v * 64 + lane] = make_uint4(pw[4 * q], pw[4 * q + 1], pw[4 * q + 2], pw[4 * q + 3]);
+    xsum[v * 64 + lane] = sum;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the staged x is visible to the wave
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t mv = magic_vgpr();
+  float acc[NJ];
+#pragma unroll
+  for (int jj = 0; jj < NJ; ++jj) acc[jj] = 0.f;
+#pragma unroll
+  for (int pp = 0; pp < NP; ++pp) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ch = 2 * (8 * pp + sl) + h;  // chunk of (g, h)
+      XChunk xc;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 t = xl[q][ch];
+        xc.p[4 * q + 0] = t.x;
+        xc.p[4 * q + 1] = t.y;
+        xc.p[4 * q + 2] = t.z;
+        xc.p[4 * q + 3] = t.w;
+      }
+      xc.sum = xsum[ch];
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj)
+        acc[jj] += affine_chunk(dot_chunk(wv[pp][h][jj], xc, mv), xc.sum, __uint_as_float(sbw[pp][jj] << 16),
+                                __uint_as_float(sbw[pp][jj] & 0xFFFF0000u));
+    }
+  }
+  float gate, up;
+  if constexpr (RG == 8) {
+    gate = sum8(acc[0]);
+    up = sum8(acc[1]);
+  } else {
+    // lanes 8r, r < 4: gate row r; r >= 4: up row r - 4, 32 lanes above
+    const float t = sum8(acc[0]);
+    auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
+    gate = t;
+    up = as_f(sw[1]);
+  }
+  if (sl == 0 && r < RG)
+    a.out[(int64_t)pr * a.n_out + i0 + r] = (uint16_t)f32_to_bf16(gate / (1.0f + expf(-gate)) * up);
 }
 
 struct DownArgs {
@@ -569,6 +786,7 @@ struct DownArgs {
   const uint16_t* b;
   int num_experts, D;
   uint16_t* y;  // [T, D]
+  const uint32_t* sb;  // tile layout: scale|bias words (w then holds the tile-layout codes)
 };
 
 // One block per group of 64/LPR output rows; wave t handles token t and walks
@@ -679,6 +897,59 @@ __global__ __launch_bounds__(64 * kPairMaxK) void down_pair_kernel(DownArgs a) {
   for (int i = 0; i < NI; ++i) {
     const float v = group_sum<16>(affine_chunk(dot_chunk(wq[i], hc, mv), hc.sum, bf16_to_f32(sv[i]),
                                                bf16_to_f32(bv[i])));
+    if (l == 0) red[j][4 * i + rg] = sc * v;
+  }
+  __syncthreads();
+  if (threadIdx.x < R) {
+    float y = 0.f;
+    for (int jj = 0; jj < a.k; ++jj) y += red[jj][threadIdx.x];
+    const int d = d0 + threadIdx.x;
+    if (d < D) a.y[(int64_t)t * D + d] = (uint16_t)f32_to_bf16(y);
+  }
+}
+
+// down_pair_kernel over tile-layout down weights [E, D, I = 512] (group 64,
+// G = 8): lane (rg, l) reads the 16-byte unit (g = l / 2, h = l % 2) of rows
+// d0 + 4i + rg, which is the same 32 codes its MLX-layout counterpart reads,
+// so the result is bit-identical to it.  One load instruction covers four
+// consecutive rows (64 contiguous bytes per (g, h)); the R rows of a wave
+// (d0 % R == 0, R | 32) fill whole 128-byte lines across its R/4 loads, which
+// are ordinary (cached) loads so the later ones find the lines the first ones
+// brought in.  The rows' scale|bias words are 4-byte loads from the group's
+// 256-byte chunk.  (Eight lanes per line with two h chunks per lane measured
+// slower: every wave then reads twice the h row.)
+template <int R>
+__global__ __launch_bounds__(64 * kPairMaxK) void down_pair_tiled_kernel(DownArgs a) {
+  constexpr int NI = R / 4;
+  __shared__ float red[kPairMaxK][R];
+  const int t = blockIdx.y;
+  const int j = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int rg = lane >> 4, l = lane & 15;
+  const int d0 = blockIdx.x * R;
+  const int D = a.D;
+  const int NCd = D / 64;
+  const int g = l >> 1, h = l & 1;
+  const int64_t p = (int64_t)t * a.k + j;
+  XChunk hc;
+  load_x_chunk(a.h + p * 512 + l * 32, hc);
+  int e = a.idx[p];
+  e = min(max(e, 0), a.num_experts - 1);
+  const float sc = a.scores[p];
+  uint4 wq[NI];
+  uint32_t sbw[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int row = min(d0 + 4 * i + rg, D - 1);
+    const int64_t chunk = ((int64_t)e * NCd + (row >> 6)) * 8 + g;
+    wq[i] = *(reinterpret_cast<const uint4*>(a.w) + ((chunk * 2 + ((row >> 5) & 1)) * 2 + h) * 32 + (row & 31));
+    sbw[i] = a.sb[chunk * 64 + (row & 63)];
+  }
+  const uint32_t mv = magic_vgpr();
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const float v = group_sum<16>(affine_chunk(dot_chunk(wq[i], hc, mv), hc.sum, __uint_as_float(sbw[i] << 16),
+                                               __uint_as_float(sbw[i] & 0xFFFF0000u)));
     if (l == 0) red[j][4 * i + rg] = sc * v;
   }
   __syncthreads();
@@ -804,20 +1075,71 @@ int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st, int bits = 4) 
   return qmoe::fail(QMOE_ERR_UNSUPPORTED, "no qmv kernel for lpr=%d nv=%d", lpr, nv);
 }
 
-template <int MODE>
 int launch_qmv_tiled(const QmvArgs& a, hipStream_t st) {
-  constexpr int outs = MODE == 1 ? 4 : 8;
-  const int64_t blocks = a.n_pairs * ((a.n_out + outs - 1) / outs);
+  const int64_t blocks = a.n_pairs * ((a.n_out + 7) / 8);
   if (blocks <= 0) return QMOE_OK;
   if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
   dim3 grid((unsigned)blocks), block(64);
   switch (a.K / 2048) {
-    case 1: qmv64_tiled_kernel<1, MODE><<<grid, block, 0, st>>>(a); break;
-    case 2: qmv64_tiled_kernel<2, MODE><<<grid, block, 0, st>>>(a); break;
-    case 3: qmv64_tiled_kernel<3, MODE><<<grid, block, 0, st>>>(a); break;
-    default: qmv64_tiled_kernel<4, MODE><<<grid, block, 0, st>>>(a); break;
+    case 1: qmv64_tiled_kernel<1><<<grid, block, 0, st>>>(a); break;
+    case 2: qmv64_tiled_kernel<2><<<grid, block, 0, st>>>(a); break;
+    case 3: qmv64_tiled_kernel<3><<<grid, block, 0, st>>>(a); break;
+    default: qmv64_tiled_kernel<4><<<grid, block, 0, st>>>(a); break;
   }
   return qmoe::launch_status("qmv64_tiled_kernel");
+}
+
+template <int RG>
+int launch_qmv_paired_rg(QmvArgs a, hipStream_t st) {
+  const int64_t nblk = a.n_out / RG;
+  const int64_t blocks = a.n_pairs * nblk;
+  if (blocks <= 0) return QMOE_OK;
+  if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
+  if (a.x_div < 1 || a.x_div > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_INVALID, "top_k out of range");
+  a.blk_div = make_fastdiv((uint32_t)nblk);
+  a.x_divf = make_fastdiv((uint32_t)a.x_div);
+  dim3 grid((unsigned)blocks), block(64);
+  switch (a.K / 2048) {
+    case 1: qmv64_paired_kernel<1, RG><<<grid, block, 0, st>>>(a); break;
+    case 2: qmv64_paired_kernel<2, RG><<<grid, block, 0, st>>>(a); break;
+    default:
+      if constexpr (RG == 4) {
+        if (a.K / 2048 == 3) qmv64_paired_kernel<3, 4><<<grid, block, 0, st>>>(a);
+        else qmv64_paired_kernel<4, 4><<<grid, block, 0, st>>>(a);
+      } else {
+        return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%d: %d indices per wave take K <= 4096", a.K, RG);
+      }
+  }
+  return qmoe::launch_status("qmv64_paired_kernel");
+}
+
+// K = 2048 n: RG indices per wave for n <= 2, four above (16 rows x n 16-byte
+// code loads per lane would pass 256 registers)
+// Indices per wave of the line-read paired kernel.
+// (four measured faster than eight at the decode shapes: 5.7 against 6.1 us at
+// one token x top-10 of 256 experts, hidden 2048; twice the waves in flight)
+#ifndef QMOE_PAIRED_LINES_RG
+#define QMOE_PAIRED_LINES_RG 4
+#endif
+
+int launch_qmv_paired(const QmvArgs& a, hipStream_t st) {
+  if (a.K <= 4096) {
+    // line reads with x staged in LDS (K = 2048 or 4096)
+    constexpr int RG = QMOE_PAIRED_LINES_RG;
+    QmvArgs b = a;
+    const int64_t nblk = a.n_out / RG;
+    const int64_t blocks = a.n_pairs * nblk;
+    if (blocks <= 0) return QMOE_OK;
+    if (blocks > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "grid too large");
+    if (a.x_div < 1 || a.x_div > 0x7FFFFFFF) return qmoe::fail(QMOE_ERR_INVALID, "top_k out of range");
+    b.blk_div = make_fastdiv((uint32_t)nblk);
+    b.x_divf = make_fastdiv((uint32_t)a.x_div);
+    dim3 grid((unsigned)blocks), block(64);
+    if (a.K == 2048) qmv64_paired_lines_kernel<1, RG><<<grid, block, 0, st>>>(b);
+    else qmv64_paired_lines_kernel<2, RG><<<grid, block, 0, st>>>(b);
+    return qmoe::launch_status("qmv64_paired_lines_kernel");
+  }
+  return launch_qmv_paired_rg<4>(a, st);
 }
 
 int check_tiled(int64_t K, int64_t rows_per_expert, const void* x, const void* wp, const void* sb) {
@@ -967,7 +1289,7 @@ extern "C" int qmoe_gather_qmv_tiles(const uint16_t* x, const int32_t* x_rows, c
   if (rc) return rc;
   QmvArgs a{x, K, x_rows, 1, experts, n_rows, (int)K, 64, wp, nullptr, nullptr, num_experts, (int)N, (int)N,
             out, sb};
-  return launch_qmv_tiled<0>(a, qmoe::as_stream(stream));
+  return launch_qmv_tiled(a, qmoe::as_stream(stream));
 }
 
 extern "C" int qmoe_moe_gate_up_swiglu_tiles(const uint16_t* x, const int32_t* idx, int64_t T, int64_t top_k,
@@ -976,12 +1298,35 @@ extern "C" int qmoe_moe_gate_up_swiglu_tiles(const uint16_t* x, const int32_t* i
   if (T < 0 || top_k <= 0 || I <= 0 || num_experts <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
   if (T == 0) return QMOE_OK;
   if (!x || !idx || !wp || !sb || !h) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
-  if (I % 4) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "I=%lld: must be a multiple of 4", (long long)I);
+  if (I % 32) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "I=%lld: the paired layout needs I %% 32 == 0", (long long)I);
   const int rc = check_tiled(K, 2 * I, x, wp, sb);
   if (rc) return rc;
   QmvArgs a{x, K, nullptr, top_k, idx, T * top_k, (int)K, 64, wp, nullptr, nullptr, num_experts, (int)I,
             (int)(2 * I), h, sb};
-  return launch_qmv_tiled<1>(a, qmoe::as_stream(stream));
+  return launch_qmv_paired(a, qmoe::as_stream(stream));
+}
+
+extern "C" int qmoe_moe_down_wsum_tiles(const uint16_t* h, const int32_t* idx, const float* scores, int64_t T,
+                                        int64_t top_k, int64_t I, const uint32_t* wp, const uint32_t* sb,
+                                        int32_t num_experts, int64_t D, uint16_t* y, void* stream) {
+  if (T < 0 || top_k <= 0 || D <= 0 || num_experts <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (T == 0) return QMOE_OK;
+  if (!h || !idx || !scores || !wp || !sb || !y) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (I != 512) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "I=%lld: the tiled down kernel takes I = 512", (long long)I);
+  if (T > 16) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "T=%lld: the fused down kernel takes at most 16 tokens", (long long)T);
+  if (top_k > kPairMaxK) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "top_k=%lld > %d", (long long)top_k, kPairMaxK);
+  if (D % 64) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "D=%lld: must be a multiple of 64", (long long)D);
+  if (D > 0x3FFFFFFF) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "D too large");
+  if (!qmoe::aligned16(h) || !qmoe::aligned16(wp) || !qmoe::aligned16(sb))
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "h, wp and sb must be 16-byte aligned");
+  DownArgs a{h, idx, scores, (int)T, (int)top_k, (int)I, 64, wp, nullptr, nullptr, num_experts, (int)D, y, sb};
+  hipStream_t st = qmoe::as_stream(stream);
+  // rows per wave as for the MLX-layout kernel: 8 for one token, 16 from two on
+  const int R = T == 1 ? 8 : 16;
+  dim3 grid((unsigned)(D / R), (unsigned)T), block((unsigned)(64 * top_k));
+  if (R == 8) down_pair_tiled_kernel<8><<<grid, block, 0, st>>>(a);
+  else down_pair_tiled_kernel<16><<<grid, block, 0, st>>>(a);
+  return qmoe::launch_status("down_pair_tiled_kernel");
 }
 
 #ifdef QMOE_QMV_STAMPS

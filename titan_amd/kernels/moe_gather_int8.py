@@ -3,9 +3,11 @@
 
 Activations are quantised per token, symmetrically: ``sx = max|x| / 127``
 (fp32), ``xi = clamp(rint(x / sx), -127, 127)``.  Per 64-wide group the kernel
-forms ``D = sum xi * q`` with ``v_mfma_i32_32x32x32_i8`` (codes 0..15 are
-valid int8 operands as they are, so no re-centring and no nibble-sum table)
-and ``R = sum xi`` exactly, then ``y = sx * sum_g (s * D + b * R)`` in fp32.
+forms ``D = sum xi * q`` with one ``v_mfma_i32_16x16x64_i8`` per 16 x 16 tile
+(codes 0..15 are valid int8 operands as they are, so no re-centring and no
+nibble-sum table) and ``R = sum xi`` exactly, then
+``y = sx * sum_g (s * D + b * R)`` in fp32.  The weights are read in the tile
+layout, repacked once per tensor: :class:`Int8Tables` holds that copy.
 
 Not exact against the unquantised product, by design: this is the one op whose
 fast path changes the numbers, so, as in the reference
@@ -21,6 +23,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import ops, stock
+from . import prepared
 from .moe_gather_ws import build_tiles
 from .registry import KernelOp, ShapeClass, shape_class
 
@@ -34,26 +37,29 @@ BITS = 4
 @dataclass(frozen=True)
 class Int8Tables:
     """Caller-owned prepared state for one weight tensor
-    (moe_gather_int8.py:189-248).  The int8 kernel reads the MLX tensors as
-    they are, so the tables hold the validated operands and no copies; their
-    presence is the caller's opt-in to the approximate path."""
+    (moe_gather_int8.py:189-248): its tile-layout repack, per (expert,
+    64-column block, group) a 2 KiB code chunk and a 256-byte chunk of
+    scale|bias words -- the operands the int8 kernel copies contiguously.  The
+    reference's tables add 18.8% of the weights (transposed scales, folded
+    bias, nibble sums); these are a permuted copy of the weights themselves,
+    shared with the bf16 path through the prepared cache.  Passing them is the
+    caller's opt-in to the approximate path."""
 
-    w: torch.Tensor
-    scales: torch.Tensor
-    biases: torch.Tensor
+    tw: ops.TileWeights
 
     @property
     def nbytes(self) -> int:
-        return 0
+        return self.tw.nbytes
 
 
 def build_tables(wq, scales, biases) -> Int8Tables:
-    """Validate and wrap one weight tensor's operands (one-time, per tensor)."""
+    """One weight tensor's tables: its tile-layout repack, built once per tensor
+    (cached by the tensors' identity, :mod:`.prepared`)."""
     if wq.dim() != 3 or scales.shape != biases.shape or scales.dim() != 3:
         raise ValueError("expected w [E, N, K/8] and scales/biases [E, N, K/64]")
     if wq.shape[-1] * 8 != scales.shape[-1] * GROUP:
         raise ValueError("w and scales disagree on K")
-    return Int8Tables(wq, scales, biases)
+    return Int8Tables(prepared.tile_weights(wq, scales, biases))
 
 
 def pick_cfg(N: int):
@@ -85,7 +91,7 @@ def hip(x, wq, scales, biases, rhs_indices, tables=None, tiles=None, *, group_si
     if tiles.tile_rows != ops.tile_rows() or tiles.num_experts != E or tiles.rows != R:
         raise ValueError("tile table does not match this call")
     xi, sx = quantize_activations(x.reshape(R, K))
-    y = ops.gather_qmm_int8_sorted(xi, sx, tables.w, tables.scales, tables.biases, tiles, None, group_size, bits)
+    y = ops.gather_qmm_int8_sorted_tiles(xi, sx, tables.tw, tiles)
     return y.reshape(R, 1, N)
 
 
@@ -96,7 +102,9 @@ def key(x, wq, scales, biases, rhs_indices, tables=None, tiles=None, *, group_si
 
 def supports(k: ShapeClass) -> bool:
     """Opt-in (tables passed), 4-bit group 64, [R, 1, K] bf16 rows, K a
-    multiple of 1024, N of 256 (moe_gather_int8.py:435-450)."""
+    multiple of 512 up to 4096 (the gate_up and the down projection; the
+    quantiser reads 16-byte runs of K/64 elements per lane), N of 256
+    (moe_gather_int8.py:435-450)."""
     if k.device != "gpu" or len(k.shapes) != 5 or len(k.extra) != 3:
         return False
     group_size, bits, has_tables = k.extra
@@ -105,7 +113,8 @@ def supports(k: ShapeClass) -> bool:
     xs, ws, ss, _bs, idx = k.shapes
     if len(ws) != 3 or len(ss) != 3 or len(idx) != 1 or k.dtypes[0] != torch.bfloat16:
         return False
-    if len(xs) != 3 or xs[1] != 1 or xs[0] != idx[0] or xs[-1] % 1024 or xs[0] < ops.SORTED_MIN_ROWS:
+    if len(xs) != 3 or xs[1] != 1 or xs[0] != idx[0] or xs[-1] % 512 or xs[-1] > 4096 \
+            or xs[0] < ops.SORTED_MIN_ROWS:
         return False
     return pick_cfg(ss[1]) is not None
 
@@ -124,6 +133,7 @@ OP = KernelOp(
         {"R": 300, "K": 1024, "N": 256, "E": 8, "bits": 4},
         {"R": 640, "K": 2048, "N": 512, "E": 16, "bits": 4},
         {"R": 40960, "K": 2048, "N": 1024, "E": 256, "bits": 4},
+        {"R": 40960, "K": 512, "N": 2048, "E": 256, "bits": 4},
     ),
     exactness="not exact: per-token int8 activations; integer parts exact, fp32 rescale",
     source="titan/kernels/moe_gather_int8.py",

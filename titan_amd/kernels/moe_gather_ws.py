@@ -1,11 +1,15 @@
 """Sorted-gather MoE matmul on bf16 MFMA (titan/kernels/moe_gather_ws.py).
 
 Replaces ``gather_qmm(..., sorted_indices=True)`` on the routed-expert prefill
-GEMMs: int4 affine weights, bf16 activations, fp32 accumulation, bf16 output,
-no precomputed tables.  The weights of a (tile, column block) are dequantised
-in registers as ``bf16_rne(fmaf(q, s, b))`` (moe_gather_ws.py:343-344) and fed
-to ``v_mfma_f32_32x32x16_bf16``; rows are tiled raggedly per expert through
-the caller-owned :class:`TileTable` (moe_gather_ws.py:159-202).
+GEMMs: int4 affine weights, bf16 activations, fp32 accumulation, bf16 output.
+The weights of a (tile, column block) are dequantised in registers as
+``bf16_rne(fmaf(q, s, b))`` (moe_gather_ws.py:343-344) and fed to
+``v_mfma_f32_32x32x16_bf16``; rows are tiled raggedly per expert through the
+caller-owned :class:`TileTable` (moe_gather_ws.py:159-202).  The weight tensor
+is read in the tile layout, repacked once per tensor and kept
+(:mod:`.prepared`, filled ahead of time by the patches' ``warmup``); with
+that cache off, the MLX-layout kernel reads the tensors as they are (the same
+bits, ~20% slower).
 
 Exactness: the reference holds its Metal kernel bit-identical to MLX's own
 sorted gather.  Here the bar is at most one bf16 ULP on live elements against
@@ -19,6 +23,7 @@ import torch
 
 from .. import ops, stock
 from ..ops import TileTable, max_tiles
+from . import prepared
 from .registry import KernelOp, ShapeClass, shape_class
 
 __all__ = ["GROUP", "BITS", "OP", "TileTable", "build_tiles", "key", "max_tiles", "hip", "pick_cfg",
@@ -30,9 +35,7 @@ BITS = 4
 
 def pick_cfg(N: int):
     """(tile rows, waves per block) of the column block that divides N, or
-    None (moe_gather_ws.py:394-400).  Eight waves cover 512 columns, four 256."""
-    if N % 512 == 0:
-        return (ops.tile_rows(), 8)
+    None (moe_gather_ws.py:394-400).  Four waves cover a 256-column block."""
     if N % 256 == 0:
         return (ops.tile_rows(), 4)
     return None
@@ -63,7 +66,11 @@ def hip(x, wq, scales, biases, rhs_indices, tiles=None, *, group_size=GROUP, bit
         tiles = build_tiles(rhs_indices, E)
     if tiles.tile_rows != ops.tile_rows() or tiles.num_experts != E or tiles.rows != R:
         raise ValueError("tile table does not match this call")
-    y = ops.gather_qmm_sorted(x.reshape(R, K), wq, scales, biases, tiles, None, group_size, bits)
+    if prepared.enabled():
+        tw = prepared.tile_weights(wq, scales, biases)
+        y = ops.gather_qmm_sorted_tiles(x.reshape(R, K), tw, tiles)
+    else:
+        y = ops.gather_qmm_sorted(x.reshape(R, K), wq, scales, biases, tiles, None, group_size, bits)
     return y.reshape(R, 1, N)
 
 

@@ -7,8 +7,8 @@ engine/patches/decode-fusion/fused_kernels.py:232-371).
                                                      else a library bf16 GEMM, fp32 out
     idx, sc = top-k of logits, softmax over the k    qmoe_router_topk
     decode  (T * k < 64, switch_layers.py:218):
-        h   = silu(x W_gate^T) * (x W_up^T)          qmoe_moe_gate_up_swiglu
-        y   = sum_j sc_j * W_down[idx_j] h_j          qmoe_moe_down_wsum
+        h   = silu(x W_gate^T) * (x W_up^T)          qmoe_moe_gate_up_swiglu_tiles
+        y   = sum_j sc_j * W_down[idx_j] h_j          qmoe_moe_down_wsum_tiles
     prefill:
         order, tiles = stable sort of the pairs       qmoe_route
         h   = SwiGLU gate_up grouped GEMM             qmoe_gather_qmm_swiglu_sorted_tiles
@@ -23,6 +23,18 @@ near-ties; everything after the selection has the same semantics.
 
 The optional shared expert (language.py:81-89: a dense SwiGLU MLP gated by
 sigmoid(x w_gate)) runs through the same kernels as a one-expert table.
+
+Resident weights (``resident``): by default one copy, in the tile layout --
+the block repacks gate_up (in the gate/up-paired row order) and down at
+construction and keeps only those, since every path it runs, decode GEMVs and
+prefill grouped GEMMs, has a tile-layout kernel.  The tile layout is made for
+the GEMMs (one contiguous 2 KiB chunk per 64 columns and group); the decode
+GEMVs read it slower than the MLX layout (at one token x top-10 of 256
+experts, hidden 2048: gate_up 5.7 against 5.0 us, down at 8 tokens 14.4
+against 11.1 us), so ``resident="both"`` keeps the MLX tensors too and
+decodes from them, at twice the memory.  Shapes outside the tile-layout
+decode kernels' envelope (hidden a multiple of 2048 up to 8192, intermediate
+512) keep the MLX tensors for decode either way.
 """
 
 from __future__ import annotations
@@ -33,12 +45,18 @@ import torch
 
 from . import ops
 
-__all__ = ["SparseMoeBlock", "SharedExpert", "DECODE_MAX_PAIRS", "ROUTER_GEMV_MAX_T"]
+__all__ = ["SparseMoeBlock", "SharedExpert", "DECODE_MAX_PAIRS", "ROUTER_GEMV_MAX_T", "tile_decode_supported"]
 
 # switch_layers.py:218: SwitchGLU sorts when indices.size >= 64
 DECODE_MAX_PAIRS = 64
 # router logits through the GEMV kernels up to this many tokens, a GEMM above
 ROUTER_GEMV_MAX_T = 16
+
+
+def tile_decode_supported(hidden: int, inter: int, group_size: int = ops.GROUP, bits: int = ops.BITS) -> bool:
+    """Do the tile-layout decode kernels (qmoe_moe_gate_up_swiglu_tiles,
+    qmoe_moe_down_wsum_tiles) take a SwiGLU MLP of this shape?"""
+    return (group_size, bits) == (ops.GROUP, ops.BITS) and hidden % 2048 == 0 and hidden <= 8192 and inter == 512
 
 
 @dataclass
@@ -60,9 +78,13 @@ class SparseMoeBlock:
     straight from the codes (the fused router, fused_kernels.py:232-260);
     ``gate_up`` = (w, scales, biases) of the
     fused [E, 2I, H] projection (gate rows first, loader.py:19-27); ``down`` =
-    (w, scales, biases) of [E, H, I].  The prefill copies of both weights are
-    repacked into the tile layout once, here (the gate_up copy in the
-    gate/up-paired row order of the SwiGLU GEMM).
+    (w, scales, biases) of [E, H, I].  Both are repacked into the tile layout
+    once, here (gate_up in the gate/up-paired row order of the SwiGLU kernels).
+    ``resident``: "tiles" keeps only that copy when the tile-layout decode
+    kernels take the shape (:func:`tile_decode_supported`); "both" also keeps
+    the MLX tensors and decodes from them (faster GEMVs, twice the memory);
+    ``prefill_tiles=False`` keeps only the MLX tensors and takes decode widths
+    only.  ``nbytes`` reports what stays resident.
 
     ``sort_min_pairs`` is where the sorted path takes over (default 64, stock
     SwitchGLU's rule).  The two paths round differently -- the decode kernels
@@ -74,7 +96,8 @@ class SparseMoeBlock:
     def __init__(self, router_weight: torch.Tensor, gate_up: tuple, down: tuple, top_k: int,
                  norm_topk_prob: bool = True, wsum_mode: str = "fast", group_size: int = ops.GROUP,
                  bits: int = ops.BITS, shared: SharedExpert | None = None, prefill_tiles: bool = True,
-                 sort_min_pairs: int = DECODE_MAX_PAIRS, router_quant: tuple = (ops.GROUP, ops.BITS)):
+                 sort_min_pairs: int = DECODE_MAX_PAIRS, router_quant: tuple = (ops.GROUP, ops.BITS),
+                 resident: str = "tiles"):
         self.router_weight = router_weight if isinstance(router_weight, torch.Tensor) else tuple(router_weight)
         self.router_quant = tuple(router_quant)
         if isinstance(self.router_weight, torch.Tensor):
@@ -83,8 +106,6 @@ class SparseMoeBlock:
             dense = ops.dequantize(*self.router_weight, *self.router_quant)
         # [H, E] contiguous: the library GEMM gets no transposed view
         self._router_dense_t = dense.t().contiguous()
-        self.gate_up = tuple(gate_up)
-        self.down = tuple(down)
         self.top_k = int(top_k)
         self.norm = bool(norm_topk_prob)
         self.wsum_mode = wsum_mode
@@ -94,16 +115,42 @@ class SparseMoeBlock:
         self.intermediate = int(gate_up[0].shape[1]) // 2
         self.gu_tiles = self.down_tiles = None
         if prefill_tiles:
-            self.gu_tiles = ops.repack_tiles(*self.gate_up, group_size, bits, swiglu_pairs=True)
-            self.down_tiles = ops.repack_tiles(*self.down, group_size, bits)
+            self.gu_tiles = ops.repack_tiles(*gate_up, group_size, bits, swiglu_pairs=True)
+            self.down_tiles = ops.repack_tiles(*down, group_size, bits)
+        if resident not in ("tiles", "both"):
+            raise ValueError(f"resident={resident!r}: 'tiles' or 'both'")
+        self.resident = resident if prefill_tiles else "mlx"
+        # decode from the same tile-layout copy when its kernels take the shape;
+        # the MLX tensors stay resident only when something still reads them
+        self.decode_tiles = self.resident == "tiles" and tile_decode_supported(self.hidden, self.intermediate,
+                                                                               group_size, bits)
+        self.gate_up = None if self.decode_tiles else tuple(gate_up)
+        self.down = None if self.decode_tiles else tuple(down)
         # the sorted (grouped GEMM) path from this many (token, expert) pairs
         # on; below it the decode kernels (which take at most 16 tokens)
         self.sort_min_pairs = int(sort_min_pairs)
         self.shared = shared
         self._shared_tiles = None
+        self._shared_decode_tiles = False
         if shared is not None and prefill_tiles:
             self._shared_tiles = (ops.repack_tiles(*shared.gate_up, group_size, bits, swiglu_pairs=True),
                                   ops.repack_tiles(*shared.down, group_size, bits))
+            S = int(shared.gate_up[0].shape[1]) // 2
+            if self.resident == "tiles" and tile_decode_supported(self.hidden, S, group_size, bits):
+                self._shared_decode_tiles = True
+                self.shared = SharedExpert(None, None, shared.gate_weight)
+
+    @property
+    def nbytes(self) -> int:
+        """Device bytes of the resident expert weights (routed and shared)."""
+        tensors = []
+        for tw in (self.gu_tiles, self.down_tiles, *(self._shared_tiles or ())):
+            if tw is not None:
+                tensors += [tw.wp, tw.sb]
+        for grp in (self.gate_up, self.down, *((self.shared.gate_up, self.shared.down) if self.shared else ())):
+            if grp is not None:
+                tensors += list(grp)
+        return sum(t.numel() * t.element_size() for t in tensors)
 
     # ------------------------------------------------------------- router
     def route_logits(self, x2: torch.Tensor) -> torch.Tensor:
@@ -128,6 +175,9 @@ class SparseMoeBlock:
                 raise ValueError("block built with prefill_tiles=False takes decode widths only (T <= 16)")
             decode = True
         if decode:
+            if self.decode_tiles:
+                h = ops.gate_up_silu_tiles(x2, self.gu_tiles, idx)
+                return ops.down_wsum_tiles(h, self.down_tiles, idx, scores)
             h = ops.gate_up_silu(x2, *self.gate_up, idx, self.group_size, self.bits)
             return ops.down_wsum(h, *self.down, idx, scores, self.group_size, self.bits)
         r = ops.route(idx, self.num_experts)
@@ -142,7 +192,11 @@ class SparseMoeBlock:
         T = x2.shape[0]
         zeros = torch.zeros(T, 1, dtype=torch.int32, device=x2.device)
         ones = torch.ones(T, 1, dtype=torch.float32, device=x2.device)
-        if T <= 16 or self._shared_tiles is None:  # the fused down kernel takes up to 16 tokens
+        if T <= 16 and self._shared_decode_tiles:  # the fused down kernel takes up to 16 tokens
+            gu_t, dn_t = self._shared_tiles
+            h = ops.gate_up_silu_tiles(x2, gu_t, zeros)
+            y = ops.down_wsum_tiles(h, dn_t, zeros, ones)
+        elif T <= 16 or self._shared_tiles is None:
             h = ops.gate_up_silu(x2, *sh.gate_up, zeros, self.group_size, self.bits)
             y = ops.down_wsum(h, *sh.down, zeros, ones, self.group_size, self.bits)
         else:

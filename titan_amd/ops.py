@@ -346,7 +346,11 @@ def gather_qmv_tiles(x: torch.Tensor, x_rows: torch.Tensor | None, experts: torc
 
 
 def gate_up_silu_tiles(x: torch.Tensor, tw: TileWeights, idx: torch.Tensor) -> torch.Tensor:
-    """:func:`gate_up_silu` over tile-layout fused gate_up weights [E, 2I, K]."""
+    """:func:`gate_up_silu` over tile-layout fused gate_up weights [E, 2I, K] in
+    the gate/up-paired row order (``repack_tiles(..., swiglu_pairs=True)``, the
+    layout of :func:`gather_qmm_swiglu_sorted_tiles`)."""
+    if not tw.swiglu_pairs:
+        raise ValueError("the decode SwiGLU kernel needs weights repacked with swiglu_pairs=True")
     x = _bf16(x, "x")
     T, K = x.shape
     if K != tw.K:
@@ -358,6 +362,22 @@ def gate_up_silu_tiles(x: torch.Tensor, tw: TileWeights, idx: torch.Tensor) -> t
     _lib.call("qmoe_moe_gate_up_swiglu_tiles", x.data_ptr(), idx.data_ptr(), T, k, K, tw.wp.data_ptr(),
               tw.sb.data_ptr(), tw.num_experts, I, h.data_ptr(), _stream(x))
     return h
+
+
+def down_wsum_tiles(h: torch.Tensor, tw: TileWeights, idx: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
+    """:func:`down_wsum` over tile-layout down weights [E, D, I]."""
+    if tw.swiglu_pairs:
+        raise ValueError("down weights are repacked in their own row order (swiglu_pairs=False)")
+    h = _bf16(h, "h")
+    T, k, I = h.shape
+    if I != tw.K:
+        raise ValueError(f"h has I={I}, the weights K={tw.K}")
+    idx = _i32(idx, "idx", h.device)
+    sc = _f32(scores, "scores", h.device)
+    y = torch.empty(T, tw.N, dtype=torch.bfloat16, device=h.device)
+    _lib.call("qmoe_moe_down_wsum_tiles", h.data_ptr(), idx.data_ptr(), sc.data_ptr(), T, k, I, tw.wp.data_ptr(),
+              tw.sb.data_ptr(), tw.num_experts, tw.N, y.data_ptr(), _stream(h))
+    return y
 
 
 def gemm_supported(K: int, N: int, group_size: int, bits: int) -> bool:
@@ -635,6 +655,7 @@ def router_logits(x: torch.Tensor, router, group_size: int = GROUP, bits: int = 
 __all__ = [
     "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "TileWeights", "Routing", "build_tiles", "route",
     "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmm_int8_sorted_tiles", "router_topk", "router_logits", "gather_qmm_swiglu_sorted_tiles", "swiglu_pair_order", "gather_qmv_tiles", "gate_up_silu_tiles",
+    "down_wsum_tiles",
     "max_tiles", "tile_rows", "unpack", "dequantize", "gather_qmv", "gather_qmm_sorted", "gather_qmm",
     "gemm_supported", "quantized_matmul", "gate_up_silu", "down_wsum", "moe_weighted_sum",
     "quantize_act_int8", "gather_qmm_int8_sorted",

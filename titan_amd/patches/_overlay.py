@@ -28,6 +28,33 @@ from .._lib import QmoeLibraryMissing, QmoeUnsupported
 logger = logging.getLogger(__name__)
 
 
+def switch_linears(model):
+    """Every QuantizedSwitchLinear reachable from ``model``: the object itself,
+    the values of containers, ``named_modules()`` when the object has it (the
+    walk of engine/patches/moe-int8/patch.py:182-198), and object attributes,
+    each object visited once."""
+    from ..switch_layers import QuantizedSwitchLinear
+
+    seen, out, stack = set(), [], [model]
+    while stack:
+        obj = stack.pop()
+        if obj is None or id(obj) in seen or isinstance(obj, (str, bytes, int, float)):
+            continue
+        seen.add(id(obj))
+        if isinstance(obj, QuantizedSwitchLinear):
+            out.append(obj)
+            continue
+        if hasattr(obj, "named_modules") and callable(obj.named_modules):
+            stack.extend(m for _, m in obj.named_modules() if m is not obj)
+        if isinstance(obj, dict):
+            stack.extend(obj.values())
+        elif isinstance(obj, (list, tuple, set)):
+            stack.extend(obj)
+        elif hasattr(obj, "__dict__") and not isinstance(obj, type):
+            stack.extend(v for v in vars(obj).values() if not callable(v) or hasattr(v, "__dict__"))
+    return out
+
+
 def arg(args, kwargs, pos, name, default=None):
     """Argument ``name`` at position ``pos`` after (x, w) of the call."""
     if len(args) > pos:

@@ -15,15 +15,19 @@ on top and takes what it wants first.
     TITAN_AMD_MOE_GATHER_WS_MIN_TOKENS=7 token floor (7 tokens x top-10 = the 64-row sort threshold)
     TITAN_AMD_MOE_GATHER_WS_MIN_ROWS=64  routed-row floor when the token count is unknown
 
-Memory: none; the tile table is built per call or passed by the caller.
+Memory: each routed weight tensor's tile-layout repack, as large as the tensor,
+built on its first call or by ``warmup(model)`` and shared with the int8
+overlay (``TITAN_AMD_TILE_CACHE=0``: none; the MLX-layout kernel runs).  The
+tile table is built per call or passed by the caller.
 """
 
 from __future__ import annotations
 
 
 from ..kernels import moe_gather_ws as _k
+from ..kernels import prepared
 from . import moe_int8
-from ._overlay import Overlay, arg
+from ._overlay import Overlay, arg, switch_linears
 
 MARKER = "_titan_amd_moe_gather_ws"
 
@@ -98,9 +102,22 @@ def stats() -> dict:
 
 
 def clear_cache() -> None:
-    """Nothing is cached."""
+    """Drop the prepared tile-layout repacks."""
+    prepared.clear_cache()
 
 
 def warmup(model=None) -> int:
-    """Nothing to precompute (no per-tensor tables)."""
-    return 0
+    """Repack every routed weight tensor the grouped GEMM would take into the
+    tile layout, ahead of the first prefill chunk.  Returns how many tensors
+    were prepared (0 with the tile cache off)."""
+    if not prepared.enabled():
+        return 0
+    n = 0
+    for m in switch_linears(model):
+        if (m.bits, m.group_size, m.mode) != (_k.BITS, _k.GROUP, "affine") or m.bias is not None:
+            continue
+        if _k.pick_cfg(m.output_dims) is None or m.input_dims % 128 or not m.weight.is_cuda:
+            continue
+        prepared.tile_weights(m.weight, m.scales, m.biases)
+        n += 1
+    return n

@@ -22,13 +22,21 @@ import torch
 from . import core, kernels, ops
 from ._lib import QmoeLibraryMissing
 
-__all__ = ["QuantizedSwitchLinear", "SwitchGLU", "swiglu"]
+__all__ = ["QuantizedSwitchLinear", "SwitchGLU", "SwiGLU", "swiglu"]
 
 
 def swiglu(gate: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     """``silu(gate) * x`` (activations.py:9-11), in fp32, one bf16 rounding."""
     g = gate.to(torch.float32)
     return (g * torch.sigmoid(g) * x.to(torch.float32)).to(x.dtype)
+
+
+class SwiGLU:
+    """The default activation module: called as ``activation(x, gate)`` with
+    the up projection first (switch_layers.py:189-194), ``silu(gate) * x``."""
+
+    def __call__(self, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        return swiglu(gate, x)
 
 
 def _gather_sort(x: torch.Tensor, indices: torch.Tensor, num_experts: int):
@@ -110,12 +118,13 @@ class SwitchGLU:
 
     def __init__(self, down_proj: QuantizedSwitchLinear, gate_up_proj: QuantizedSwitchLinear | None = None,
                  gate_proj: QuantizedSwitchLinear | None = None, up_proj: QuantizedSwitchLinear | None = None,
-                 activation=swiglu):
+                 activation=None):
         if gate_up_proj is None and (gate_proj is None or up_proj is None):
             raise ValueError("need gate_up_proj, or both gate_proj and up_proj")
         self.gate_up_proj, self.gate_proj, self.up_proj = gate_up_proj, gate_proj, up_proj
         self.down_proj = down_proj
-        self.activation = activation
+        # called as activation(x_up, x_gate), the reference's operand order
+        self.activation = SwiGLU() if activation is None else activation
 
     @property
     def num_experts(self) -> int:
@@ -134,7 +143,7 @@ class SwitchGLU:
         else:
             x_up = self.up_proj(x, idx, sorted_indices=do_sort, tiles=tiles)
             x_gate = self.gate_proj(x, idx, sorted_indices=do_sort, tiles=tiles)
-        x = self.down_proj(self.activation(x_gate, x_up), idx, sorted_indices=do_sort, tiles=tiles)
+        x = self.down_proj(self.activation(x_up, x_gate), idx, sorted_indices=do_sort, tiles=tiles)
         if do_sort:
             x = _scatter_unsort(x, inv_order, indices.shape)
         return x.squeeze(-2)
