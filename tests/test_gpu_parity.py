@@ -609,7 +609,7 @@ def _prefill_routed(dev, orc, tokens, cfg=3):
 @pytest.mark.parametrize("tokens", [4096, 8192])
 def test_sorted_gemm_tiles_prefill_sampled(dev, orc, tokens):
     """The tile-layout grouped GEMM the bench times for workload 3, at its
-    full size (4096 tokens, 477 tiles) and at 8192 tokens, where the tile
+    full size (4096 tokens, 479 tiles) and at 8192 tokens, where the tile
     count passes the 512 the heavy-first ranking holds and the kernel walks
     tiles in table order."""
     say(f"sorted GEMM tiles, {tokens} tokens x top-10 Zipf, sampled rows")
@@ -629,6 +629,54 @@ def test_sorted_gemm_tiles_prefill_sampled(dev, orc, tokens):
         ym = ops.gather_qmm_sorted(bf16_t(wl["x"], dev), words_t(wl["w"], dev), bf16_t(wl["s"], dev),
                                    bf16_t(wl["b"], dev), r.tiles, x_rows=lhs)
         assert torch.equal(ym, y)
+
+
+def test_grouped_gemms_repeat_and_replay(dev, orc):
+    """Back-to-back calls of the grouped GEMMs on one tile table (bf16,
+    SwiGLU, int8, as a block's projections share it) give identical results,
+    and a captured graph of the GEMM replays to the eager result every time,
+    with eager work on the same table between replays."""
+    say("grouped GEMMs: repeat calls and graph replays")
+    wl, r, lhs, order, srt, off = _prefill_routed(dev, orc, 1024)
+    t = r.tiles
+    xt = bf16_t(wl["x"], dev)
+    tw = ops.repack_tiles(words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev))
+    twp = ops.repack_tiles(words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev), swiglu_pairs=True)
+    xi, sx = ops.quantize_act_int8(xt)
+    runs = {
+        "bf16": lambda: ops.gather_qmm_sorted_tiles(xt, tw, t, x_rows=lhs),
+        "swiglu": lambda: ops.gather_qmm_swiglu_sorted_tiles(xt, twp, t, x_rows=lhs),
+        "int8": lambda: ops.gather_qmm_int8_sorted_tiles(xi, sx, tw, t, x_rows=lhs),
+    }
+    first = {}
+    for rep in range(3):
+        for name, f in runs.items():
+            y = f()
+            torch.cuda.synchronize()
+            if rep == 0:
+                first[name] = y.clone()
+            else:
+                assert torch.equal(y, first[name]), (name, rep)
+    rows = _sample_rows(off, int(wl["idx"].size), 128, np.random.default_rng(9))
+    k = wl["idx"].shape[1]
+    ref64, _ = orc.gather_qmm_rows(wl["x"], (order[rows] // k).astype(np.int32), srt[rows], wl["w"], wl["s"],
+                                   wl["b"], deq="bf16")
+    assert_close_bf16(orc, bits(first["bf16"])[rows], ref64, what="gemm tiles 1024 tokens")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        runs["bf16"]()  # warm the allocator off the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        yg = runs["bf16"]()
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, first["bf16"]), rep
+        runs["int8"]()  # eager work on the same table between replays
+        torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("tokens", [4096, 8192])
