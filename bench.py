@@ -609,7 +609,42 @@ def setup_cfg4(args, dev):
                           t.ntiles.data_ptr(), t.maxt, out.data_ptr(), st)
         return f
 
+    # the down projection of the same 40960 routed rows (h [40960, 512] in
+    # sorted order, W [256, 2048, 512]): int8 (quantiser + GEMM) against the
+    # bf16 GEMM, as the reference reports both projections
+    # (engine/patches/moe-int8/REPORT.md:230-239)
+    rows = T * wl["idx"].shape[1]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(404)
+    dsets = [ops.repack_tiles(random_like_words((256, 2048, 64), dev, gen), random_scales((256, 2048, 8), dev, gen),
+                              random_biases((256, 2048, 8), dev, gen)) for _ in range(2)]
+    h = (torch.randn(rows, 512, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    hi = torch.empty(rows, 512, dtype=torch.int8, device=dev)
+    hs = torch.empty(rows, dtype=torch.float32, device=dev)
+    yd = torch.empty(rows, 2048, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+
+    def mk_down(i, int8):
+        tw = dsets[i % len(dsets)]
+
+        def f():
+            st = torch.cuda.current_stream().cuda_stream
+            if int8:
+                ops._lib.call("qmoe_quantize_act_int8", h.data_ptr(), rows, 512, hi.data_ptr(), hs.data_ptr(), st)
+                ops._lib.call("qmoe_gather_qmm_int8_sorted_tiles", hi.data_ptr(), hs.data_ptr(), None, rows, 512,
+                              tw.wp.data_ptr(), tw.sb.data_ptr(), 256, 2048, t.offsets.data_ptr(),
+                              t.tile_row.data_ptr(), t.tile_exp.data_ptr(), t.ntiles.data_ptr(), t.maxt,
+                              yd.data_ptr(), st)
+            else:
+                ops._lib.call("qmoe_gather_qmm_sorted_tiles", h.data_ptr(), None, rows, 512, tw.wp.data_ptr(),
+                              tw.sb.data_ptr(), 256, 2048, t.offsets.data_ptr(), t.tile_row.data_ptr(),
+                              t.tile_exp.data_ptr(), t.ntiles.data_ptr(), t.maxt, yd.data_ptr(), st)
+        return f
+
+    down_flops = 2 * rows * 2048 * 512
     return wl, [mk(i) for i in range(L)], {
+        "extras": [("down_int8", [mk_down(i, True) for i in range(L)], down_flops),
+                   ("down_bf16", [mk_down(i, False) for i in range(L)], down_flops)],
         "flops": synth.algorithmic_flops(4, wl), "bound": "mfma", "peak_tflops": INT8_PEAK_TOPS,
         "peak_key": "int8_mfma_TOPs", "kernel": "quant_act_kernel + gemm_int8_kernel<true>", "sets": len(sets),
         "steps": prefill_steps(args),
@@ -1020,6 +1055,11 @@ def main():
             sec_alt, _ta = timer(args)(alt, steps, args.warmup, dev)
             res[label] = round(sec_alt * 1e6, 3)
             del alt, _ta
+        for label, ex, ex_flops in meta.get("extras", ()):
+            sec_ex, _te = timer(args)(ex, steps, args.warmup, dev)
+            res[label] = {"us_per_call": round(sec_ex * 1e6, 3), "TOP/s": round(ex_flops / sec_ex / 1e12, 1),
+                          "flops_per_call": ex_flops}
+            del ex, _te
         results[cfg] = res
         print(f"[bench] workload {cfg}: {res}", file=sys.stderr, flush=True)
         if cfg == 1:

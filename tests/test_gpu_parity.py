@@ -364,7 +364,8 @@ def test_quantize_act_int8_bit_exact(dev, orc):
 
 
 @pytest.mark.parametrize("E,N,K,R", [(8, 256, 1024, 300), (16, 512, 2048, 640), (4, 768, 4096, 200),
-                                     (8, 256, 1536, 90)])
+                                     (8, 256, 1536, 90),
+                                     (16, 2048, 512, 700)])  # the prefill down projection's shape (K = I = 512)
 def test_sorted_gemm_int8(dev, orc, E, N, K, R):
     say(f"int8 sorted GEMM E={E} N={N} K={K} R={R}")
     w, s, b, ids, x = _sorted_problem(E * 17 + R, E, N, K, R)
@@ -423,6 +424,36 @@ def test_sorted_gemm_int8_cfg4_sampled(dev, orc):
     ref64, _ = orc.gather_qmm_int8_rows(rxi, rsx, (order[rows] // k).astype(np.int32), srt[rows], wl["w"],
                                         wl["s"], wl["b"])
     assert_close_bf16(orc, bits(y)[rows], ref64, what=f"cfg4 {rows.size} rows")
+
+
+def test_sorted_gemm_int8_down_prefill_sampled(dev, orc):
+    """The int8 grouped GEMM on the prefill down projection at full size:
+    4096 tokens x top-10 Zipf routed rows (40960, sorted by expert, no
+    gather), h [40960, 512] -> [40960, 2048] with W [256, 2048, 512] int4 g64
+    (K = I = 512), sampled rows against the fake-quant golden, and the bf16
+    GEMM on the same rows against its fp64 golden."""
+    say("int8 + bf16 sorted GEMM, down projection 40960 x 512 -> 2048, sampled rows")
+    wl = synth.make(4)
+    T, k = wl["idx"].shape
+    rng = np.random.default_rng(512)
+    w, s, b = synth.quant_weights(rng, (256, 2048), 512)
+    order, _, srt = orc.route_sort(wl["idx"], 256)
+    R = T * k
+    h = synth.bf16_bits((rng.normal(size=(R, 512)) * 0.5).astype(np.float32))
+    tiles = ops.build_tiles(i32_t(srt, dev), 256)
+    ht = bf16_t(h, dev)
+    tw = ops.repack_tiles(words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev))
+    hi, hs = ops.quantize_act_int8(ht)
+    y8 = ops.gather_qmm_int8_sorted_tiles(hi, hs, tw, tiles)
+    y16 = ops.gather_qmm_sorted_tiles(ht, tw, tiles)
+    torch.cuda.synchronize()
+    off = np.searchsorted(srt, np.arange(257), side="left")
+    rows = _sample_rows(off, R, 256, np.random.default_rng(5))
+    rxi, rsx = orc.quant_act_int8(h[rows])
+    ref8, _ = orc.gather_qmm_int8_rows(rxi, rsx, None, srt[rows], w, s, b)
+    assert_close_bf16(orc, bits(y8)[rows], ref8, what=f"int8 down {rows.size} rows")
+    ref16, _ = orc.gather_qmm_rows(h[rows], None, srt[rows], w, s, b, deq="bf16")
+    assert_close_bf16(orc, bits(y16)[rows], ref16, what=f"bf16 down {rows.size} rows")
 
 
 # ---------------------------------------------------------------- tile layout
