@@ -68,3 +68,18 @@ def test_loaded_block_matches_direct_block(dev, orc, ckpt, layer, T):
     torch.cuda.synchronize()
     assert np.array_equal(bits(y), bits(yr))
     assert torch.isfinite(y.float()).all()
+
+
+def test_loader_passes_the_residency_choice(dev, ckpt):
+    """``load_moe_block(resident=...)`` reaches the block: "both" keeps the
+    MLX tensors beside the tile-layout copy and decodes from them; "tiles"
+    (the default) keeps one copy where the tile-layout decode kernels take the
+    shape -- not this checkpoint's (H = 1024, I = 256), so both keep both."""
+    d, layers, config = ckpt
+    prefix = f"{ROOT}.0.mlp"
+    say(f"loaded MoE block {prefix}: resident tiles / both")
+    one = loader.load_moe_block(d, prefix, device=dev)
+    two = loader.load_moe_block(d, prefix, device=dev, resident="both")
+    assert one.resident == "tiles" and two.resident == "both"
+    assert not two.decode_tiles and not one.decode_tiles
+    assert two.nbytes == one.nbytes

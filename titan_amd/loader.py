@@ -307,11 +307,13 @@ def load_moe_tensors(tensors: dict, plan: MoeLayerPlan, device="cpu") -> dict:
 
 
 def load_moe_block(model_dir, prefix: str | None = None, device="cuda", *, tensors=None, config=None,
-                   plans=None, wsum_mode: str = "fast", prefill_tiles: bool = True):
+                   plans=None, wsum_mode: str = "fast", prefill_tiles: bool = True, resident: str = "tiles"):
     """Load one MoE layer (the first one, or the one at ``prefix``) into a
     :class:`~titan_amd.moe_block.SparseMoeBlock` on ``device``.  ``top_k``
     and ``norm_topk_prob`` come from the config's text section
-    (``num_experts_per_tok``, default 8; ``norm_topk_prob``, default True)."""
+    (``num_experts_per_tok``, default 8; ``norm_topk_prob``, default True).
+    ``resident`` is the block's: "tiles" keeps one tile-layout copy of the
+    expert weights, "both" keeps the MLX tensors for decode as well."""
     import torch
 
     from . import moe_block
@@ -349,7 +351,7 @@ def load_moe_block(model_dir, prefix: str | None = None, device="cuda", *, tenso
     norm = bool(text.get("norm_topk_prob", True))
     return moe_block.SparseMoeBlock(router, gu, dn, top_k, norm_topk_prob=norm, wsum_mode=wsum_mode,
                                     group_size=spec["group_size"], bits=spec["bits"], shared=shared,
-                                    prefill_tiles=prefill_tiles,
+                                    prefill_tiles=prefill_tiles, resident=resident,
                                     router_quant=(rspec["group_size"], rspec["bits"]))
 
 
