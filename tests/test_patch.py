@@ -204,7 +204,12 @@ def test_switch_linears_finds_nested_layers():
             for i, kd in enumerate(self.kids):
                 yield str(i), kd
 
-    model = {"blocks": [glu, Mod([c, glu])], "other": "x"}
+    import types
+
+    # a Python module and a class as attributes are not entered (the walk
+    # would otherwise cover the module's whole namespace)
+    holder = types.SimpleNamespace(mod=torch, cls=QuantizedSwitchLinear, layer=c)
+    model = {"blocks": [glu, Mod([c, glu])], "other": "x", "holder": holder}
     found = switch_linears(model)
     assert sorted(map(id, found)) == sorted(map(id, (a, b, c)))
     # CPU tensors: nothing to prepare, the walk still completes

@@ -32,13 +32,19 @@ def switch_linears(model):
     """Every QuantizedSwitchLinear reachable from ``model``: the object itself,
     the values of containers, ``named_modules()`` when the object has it (the
     walk of engine/patches/moe-int8/patch.py:182-198), and object attributes,
-    each object visited once."""
+    each object visited once.  Tensors, Python modules and classes are not
+    entered."""
+    import types
+
+    import torch
+
     from ..switch_layers import QuantizedSwitchLinear
 
+    leaves = (str, bytes, int, float, torch.Tensor, types.ModuleType, type)
     seen, out, stack = set(), [], [model]
     while stack:
         obj = stack.pop()
-        if obj is None or id(obj) in seen or isinstance(obj, (str, bytes, int, float)):
+        if obj is None or id(obj) in seen or isinstance(obj, leaves):
             continue
         seen.add(id(obj))
         if isinstance(obj, QuantizedSwitchLinear):
@@ -50,7 +56,7 @@ def switch_linears(model):
             stack.extend(obj.values())
         elif isinstance(obj, (list, tuple, set)):
             stack.extend(obj)
-        elif hasattr(obj, "__dict__") and not isinstance(obj, type):
+        elif hasattr(obj, "__dict__"):
             stack.extend(v for v in vars(obj).values() if not callable(v) or hasattr(v, "__dict__"))
     return out
 
