@@ -1,7 +1,7 @@
 """numpy front end to the C oracle.  TEST INFRASTRUCTURE ONLY.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg
-import this module; ``titan_amd`` never does.  It is the checker the HIP path is
+import this module; ``titan_amd`` never does.  It is the oracle the HIP path is
 compared against, never a thing that is shipped or measured as the product.
 
 Every wrapper forwards to ``oracle/qmoe_oracle.c``; the C file cites the

@@ -2,7 +2,7 @@
  * CPU oracle for the quantized MoE gather_qmm path.  TEST INFRASTRUCTURE ONLY.
  *
  * This is a plain-C restatement of the arithmetic of MLX-affine quantized
- * matmuls as the reference calls them.  It is the checker: only tests/,
+ * matmuls as the reference calls them.  It is test infrastructure: only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it, and the
  * product (titan_amd/) never links, imports or calls it.
  *

@@ -2,7 +2,7 @@
 
 Markers: ``gpu`` tests need a ROCm GPU and the built libqmoe.so; everything
 else runs on the CPU.  The repository root goes on sys.path so tests can
-import ``titan_amd`` and the oracle (``oracle/oracle.py``, the checker).
+import ``titan_amd`` and the oracle (``oracle/oracle.py``).
 """
 
 import sys
