@@ -188,6 +188,7 @@ struct ICtx {
   uint32_t lds;
   int G;
   int rh, cw, lane;  // row parity and column group: wave-uniform
+  int tsub;          // the tile's 32-row subtiles
 };
 
 // 16 codes (two words, k order 0..15) -> 16 int8 in natural k order.
@@ -279,8 +280,60 @@ __device__ __forceinline__ BState load_bstate(const ICtx<TILED>& c, const char* 
   return b;
 }
 
-// Main loop over the groups of one tile whose rows fill MSUB 32-row subtiles:
-// the wave has MSUB 16-row subtiles (tile subtiles 2j + rh).  Per group and
+// One group's MFMAs and rescales for the wave's MSUB (>= 1) subtiles, with
+// the copies of group g + kStages - 1 issued after the first subtile's MFMAs.
+template <bool TILED, int MSUB>
+__device__ __forceinline__ void group_i8(const ICtx<TILED>& c, char* smem, const char* st, int g, int aoff, Acc& acc) {
+  using C = ICfg<TILED>;
+  const int G = c.G;
+  const int l16 = c.lane & 15, qq = c.lane >> 4;
+  const BState bs = load_bstate<TILED>(c, st, g);
+  if constexpr (TILED) {
+    // the parity-0 wave keeps its columns' biases of group g for the bias term
+    if (!c.rh && qq == 0) {
+      uint16_t* bl = reinterpret_cast<uint16_t*>(smem + C::kBiasOff) + (c.cw * kMaxG + g) * 32;
+#pragma unroll
+      for (int jj = 0; jj < kJJ; ++jj) bl[16 * jj + l16] = (uint16_t)bs.bias[jj];
+    }
+  }
+  const char* abuf = st + C::kAOff + aoff;
+  i32x4_t dc[kJJ], dn[kJJ];
+  {
+    const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf);
+#pragma unroll
+    for (int jj = 0; jj < kJJ; ++jj) {
+      const i32x4_t z = {};
+      dc[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bs.bq[jj], z, 0, 0, 0);
+    }
+  }
+  issue_group<TILED>(c, min(g + kStages - 1, G - 1));
+#pragma unroll
+  for (int j = 0; j < MSUB; ++j) {
+    if (j + 1 < MSUB) {
+      const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf + (j + 1) * 32 * 64);
+#pragma unroll
+      for (int jj = 0; jj < kJJ; ++jj) {
+        const i32x4_t z = {};
+        dn[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bs.bq[jj], z, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < kJJ; ++jj) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[j][jj][r] = __builtin_fmaf(bs.sc[jj], (float)dc[jj][r], acc[j][jj][r]);
+      // keep the rescale here, between this subtile's and the next one's
+      // MFMAs, rather than sunk to the end of the group
+      asm volatile("" : "+v"(acc[j][jj]));
+    }
+#pragma unroll
+    for (int jj = 0; jj < kJJ; ++jj) dc[jj] = dn[jj];
+  }
+}
+
+// Main loop over the groups of one tile: the wave has MSUB 16-row subtiles
+// holding valid rows (tile subtiles 2j + rh, j < MSUB; a parity-1 wave has
+// one fewer when the tile's last 32 rows hold 16 or fewer, none on a tile of
+// at most 16 rows, and still copies, waits and sums rows).  Per group and
 // 16 x 16 subtile one v_mfma_i32_16x16x64_i8 covers the whole group; lane
 // quarter qq supplies group elements 16qq .. +15 of its row (A: unit qq of the
 // activation row) and of its column (B: code words 2(qq%2), +1 of the chunk
@@ -303,50 +356,11 @@ __device__ __forceinline__ void tile_loop_i8(const ICtx<TILED>& c, char* smem, A
     // the stage that group g + kStages - 1 overwrites
     __builtin_amdgcn_s_barrier();
     const char* st = smem + (g % kStages) * C::kStageBytes;
-    const BState bs = load_bstate<TILED>(c, st, g);
-    if constexpr (TILED) {
-      // the parity-0 wave keeps its columns' biases of group g for the bias term
-      if (!c.rh && qq == 0) {
-        uint16_t* bl = reinterpret_cast<uint16_t*>(smem + C::kBiasOff) + (c.cw * kMaxG + g) * 32;
-#pragma unroll
-        for (int jj = 0; jj < kJJ; ++jj) bl[16 * jj + l16] = (uint16_t)bs.bias[jj];
-      }
-    }
-    const char* abuf = st + C::kAOff + aoff;
-    i32x4_t dc[kJJ], dn[kJJ];
-    {
-      const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf);
-#pragma unroll
-      for (int jj = 0; jj < kJJ; ++jj) {
-        const i32x4_t z = {};
-        dc[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bs.bq[jj], z, 0, 0, 0);
-      }
-    }
-    issue_group<TILED>(c, min(g + kStages - 1, G - 1));
-#pragma unroll
-    for (int j = 0; j < MSUB; ++j) {
-      if (j + 1 < MSUB) {
-        const i32x4_t af = *reinterpret_cast<const i32x4_t*>(abuf + (j + 1) * 32 * 64);
-#pragma unroll
-        for (int jj = 0; jj < kJJ; ++jj) {
-          const i32x4_t z = {};
-          dn[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bs.bq[jj], z, 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int jj = 0; jj < kJJ; ++jj) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][jj][r] = __builtin_fmaf(bs.sc[jj], (float)dc[jj][r], acc[j][jj][r]);
-        // keep the rescale here, between this subtile's and the next one's
-        // MFMAs, rather than sunk to the end of the group
-        asm volatile("" : "+v"(acc[j][jj]));
-      }
-#pragma unroll
-      for (int jj = 0; jj < kJJ; ++jj) dc[jj] = dn[jj];
-    }
+    if constexpr (MSUB == 0) issue_group<TILED>(c, min(g + kStages - 1, G - 1));
+    else group_i8<TILED, MSUB>(c, smem, st, g, aoff, acc);
     // exact row sums of the group: the parity-1 wave of column group cw takes
     // tile subtile cw (16 int8 per lane, four lane quarters per row)
-    if (c.rh && c.cw < 2 * MSUB) {
+    if (c.rh && c.cw < 2 * c.tsub) {
       const i32x4_t af = *reinterpret_cast<const i32x4_t*>(st + C::kAOff + c.cw * 16 * 64 + unit_off);
       int part = 0;
 #pragma unroll
@@ -532,13 +546,17 @@ __device__ __forceinline__ void run_unit_i8(const Int8Args& a, char* smem, int t
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
 
-  switch (msub) {
+  // the wave's 16-row subtiles that hold valid rows: rows 32j + 16rh .. +15
+  c.tsub = msub;
+  const int nsub = (valid - 16 * c.rh + 31) / 32;  // wave-uniform, 0 only for parity 1
+  switch (nsub) {
+    case 0: tile_loop_i8<TILED, 0>(c, smem, acc); break;
     case 1: tile_loop_i8<TILED, 1>(c, smem, acc); break;
     case 2: tile_loop_i8<TILED, 2>(c, smem, acc); break;
     case 3: tile_loop_i8<TILED, 3>(c, smem, acc); break;
     default: tile_loop_i8<TILED, 4>(c, smem, acc); break;
   }
-  static_assert(kMaxSub == 4, "tile_loop_i8 is instantiated for 1..4 subtiles per parity");
+  static_assert(kMaxSub == 4, "tile_loop_i8 is instantiated for 0..4 subtiles per parity");
   __syncthreads();  // row sums and sx visible to every wave; the ring is free
   finish_tile<TILED>(a, smem, c, acc, e, row0, valid, msub, nblk);
 }
