@@ -76,6 +76,10 @@ def test_unsupported_configurations_say_so(L):
     rc = L.qmoe_gather_qmm_sorted(dummy, None, 10, 2048, dummy, dummy, dummy, 8, 200, 64, 4, dummy, dummy,
                                   dummy, dummy, 10, dummy, None)
     assert rc == _lib.ERR_UNSUPPORTED and "N=200" in _lib.last_error()
+    # the grouped GEMMs' epilogue addresses rows with 32-bit offsets: N <= 2^24
+    rc = L.qmoe_gather_qmm_sorted_tiles(dummy, None, 10, 2048, dummy, dummy, 8, (1 << 24) + 256, dummy, dummy,
+                                        dummy, dummy, 10, dummy, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "too large" in _lib.last_error()
     rc = L.qmoe_route(dummy, 10, 8, 128, dummy, dummy, dummy, dummy, dummy, dummy, dummy, 100, None, 0, None)
     assert rc == _lib.ERR_WORKSPACE
 

@@ -518,7 +518,8 @@ int check_common(const uint16_t* x, int64_t n_rows, int64_t K, int32_t num_exper
   if (N % kBN) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "N=%lld: must be a multiple of %d", (long long)N, kBN);
   if (!qmoe::aligned16(x)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "x must be 16-byte aligned");
   if (!qmoe::aligned16(out)) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "out must be 16-byte aligned");
-  if (K > 0x7FFFFFFF || N > 0x7FFFFFFF || n_rows > 0x7FFFFFFF)
+  // the epilogue addresses a tile's rows with 32-bit offsets row * N, row < kBM
+  if (K > 0x7FFFFFFF || N > (1 << 24) || n_rows > 0x7FFFFFFF)
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "sizes too large");
   return QMOE_OK;
 }
