@@ -105,3 +105,30 @@ def test_peaks_library_exports_its_header():
     assert names and set(names) <= exported, (names, exported)
     L = ctypes.CDLL(str(build.PEAKS_LIB))
     assert L.qmoe_peak_stream_blocks() > 0 and L.qmoe_peak_mfma_waves() > 0
+
+
+def test_header_is_plain_c_and_a_c_program_links(tmp_path):
+    """The boundary a C, cgo or FFI caller binds: the headers compile as
+    C11 with warnings as errors, and a C program links libqmoe.so, reads the
+    ABI version and gets QMOE_ERR_INVALID plus a message for a null pointer
+    (host-side checks only: no device is touched)."""
+    import shutil
+
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    src = tmp_path / "probe.c"
+    src.write_text(
+        '#include <stdio.h>\n#include "qmoe.h"\n#include "qmoe_peaks.h"\n'
+        "int main(void) {\n"
+        "  if (qmoe_abi_version() != QMOE_ABI_VERSION) return 2;\n"
+        "  int rc = qmoe_gather_qmv(NULL, NULL, NULL, 4, 2048, NULL, NULL, NULL, 8, 128, 64, 4, NULL, NULL);\n"
+        '  printf("%d %s\\n", rc, qmoe_last_error());\n'
+        "  return rc == QMOE_ERR_INVALID ? 0 : 3;\n"
+        "}\n")
+    exe = tmp_path / "probe"
+    libdir = str(_lib.LIB_PATH.parent)
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", str(HEADER.parent),
+                    str(src), "-L", libdir, "-lqmoe", f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0, out
+    assert "null" in out.stdout
