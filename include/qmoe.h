@@ -337,8 +337,8 @@ int qmoe_router_logits(const uint16_t* x, int64_t T, int64_t K,
 /* Router logits in fp32 from a dense bf16 router weight [E, K] (the
  * unquantised nn.Linear gate, qwen3_5_moe/language.py:52, 61):
  * logits[t, e] = sum_k x[t, k] * W[e, k], fp32 accumulation.  K % 8 == 0.
- * One wave per (token, expert): meant for decode widths; a prefill caller
- * uses a GEMM library. */
+ * Any T: one wave per (token, expert) at decode widths, a tiled bf16 MFMA
+ * GEMM from 48 tokens on (when E >= 32 and K % 128 == 0). */
 int qmoe_router_logits_dense(const uint16_t* x, int64_t T, int64_t K,
                              const uint16_t* w, int64_t E, float* logits,
                              void* stream);

@@ -59,7 +59,7 @@ def test_loaded_block_matches_direct_block(dev, orc, ckpt, layer, T):
     else:
         assert np.array_equal(bits(blk.router_weight), a["router"])
         want_router = a["router"]
-    assert np.array_equal(bits(blk._router_dense_t.t()), want_router)
+    assert np.array_equal(bits(blk._router_dense), want_router)
     assert (blk.shared is not None) == ("sg" in a)
     ref = _direct(a, dev, k)
     rng = np.random.default_rng(T + layer)

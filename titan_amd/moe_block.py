@@ -3,8 +3,8 @@
 Qwen3_5MoeSparseMoeBlock.__call__, with the fused router of
 engine/patches/decode-fusion/fused_kernels.py:232-371).
 
-    logits  = x @ W_router^T, fp32                   qmoe_router_logits[_dense] (T <= 16),
-                                                     else a library bf16 GEMM, fp32 out
+    logits  = x @ W_router^T, fp32                   qmoe_router_logits (quantized router,
+                                                     T <= 16), else qmoe_router_logits_dense
     idx, sc = top-k of logits, softmax over the k    qmoe_router_topk
     decode  (T * k < 64, switch_layers.py:218):
         h   = silu(x W_gate^T) * (x W_up^T)          qmoe_moe_gate_up_swiglu_tiles
@@ -49,7 +49,9 @@ __all__ = ["SparseMoeBlock", "SharedExpert", "DECODE_MAX_PAIRS", "ROUTER_GEMV_MA
 
 # switch_layers.py:218: SwitchGLU sorts when indices.size >= 64
 DECODE_MAX_PAIRS = 64
-# router logits through the GEMV kernels up to this many tokens, a GEMM above
+# a quantized router's logits come from its codes up to this many tokens, and
+# from its dequantised bf16 copy above (qmoe_router_logits_dense, a tiled MFMA
+# GEMM from 48 tokens on)
 ROUTER_GEMV_MAX_T = 16
 
 
@@ -101,11 +103,10 @@ class SparseMoeBlock:
         self.router_weight = router_weight if isinstance(router_weight, torch.Tensor) else tuple(router_weight)
         self.router_quant = tuple(router_quant)
         if isinstance(self.router_weight, torch.Tensor):
-            dense = self.router_weight.to(torch.bfloat16)
+            dense = self.router_weight.to(torch.bfloat16).contiguous()
         else:  # prefill logits: a GEMM over the weights dequantised once (bf16(fma(q, s, b)))
             dense = ops.dequantize(*self.router_weight, *self.router_quant)
-        # [H, E] contiguous: the library GEMM gets no transposed view
-        self._router_dense_t = dense.t().contiguous()
+        self._router_dense = dense  # [E, H]
         self.top_k = int(top_k)
         self.norm = bool(norm_topk_prob)
         self.wsum_mode = wsum_mode
@@ -157,8 +158,7 @@ class SparseMoeBlock:
         """fp32 router logits [T, E] for tokens x2 [T, H]."""
         if x2.shape[0] <= ROUTER_GEMV_MAX_T:
             return ops.router_logits(x2, self.router_weight, *self.router_quant)
-        # bf16 x bf16 products are exact in fp32; fp32 accumulation and output
-        return torch.mm(x2, self._router_dense_t, out_dtype=torch.float32)
+        return ops.router_logits(x2, self._router_dense)
 
     def route(self, x2: torch.Tensor):
         """(idx int32 [T, k], scores fp32 [T, k]) for tokens x2 [T, H]."""
@@ -204,10 +204,7 @@ class SparseMoeBlock:
             tiles = ops.build_tiles(zeros.reshape(-1), 1)
             h = ops.gather_qmm_swiglu_sorted_tiles(x2, gu_t, tiles)
             y = ops.gather_qmm_sorted_tiles(h, dn_t, tiles)
-        if T <= ROUTER_GEMV_MAX_T:
-            z = ops.router_logits(x2, sh.gate_weight)
-        else:
-            z = torch.matmul(x2.float(), sh.gate_weight.float().t())
+        z = ops.router_logits(x2, sh.gate_weight)
         return (torch.sigmoid(z) * y.float()).to(torch.bfloat16)
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
