@@ -151,23 +151,37 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(int32_t* __res
   if (tid == 0) bad[0] = nbad;
   int total;
   int run = block_exclusive_scan(local, lds, &total);
-  // an expert's offset is the prefix at its chunk-0 entry, index e * nchunks
-  if (seg <= kSegMax) {
+  // an expert's offset is the prefix at its chunk-0 entry, index e * nchunks;
+  // the thread's (expert, chunk) position advances with its index (one
+  // division per thread, not one per entry)
+  if (nchunks > 0) {
+    int64_t e = lo / nchunks;
+    int ch = (int)(lo - e * nchunks);
+    if (seg <= kSegMax) {
 #pragma unroll
-    for (int i = 0; i < kSegMax; ++i) {
-      const int64_t idx = lo + i;
-      if (idx < hi && idx < Lmain) {
-        counts[idx] = run;
-        if (idx % nchunks == 0) off[idx / nchunks] = run;
-        run += v[i];
+      for (int i = 0; i < kSegMax; ++i) {
+        const int64_t idx = lo + i;
+        if (idx < hi && idx < Lmain) {
+          counts[idx] = run;
+          if (ch == 0) off[e] = run;
+          run += v[i];
+        }
+        if (++ch == nchunks) {
+          ch = 0;
+          ++e;
+        }
       }
-    }
-  } else {
-    for (int64_t idx = lo; idx < hi && idx < Lmain; ++idx) {
-      const int c = counts[idx];
-      counts[idx] = run;
-      if (idx % nchunks == 0) off[idx / nchunks] = run;
-      run += c;
+    } else {
+      for (int64_t idx = lo; idx < hi && idx < Lmain; ++idx) {
+        const int c = counts[idx];
+        counts[idx] = run;
+        if (ch == 0) off[e] = run;
+        run += c;
+        if (++ch == nchunks) {
+          ch = 0;
+          ++e;
+        }
+      }
     }
   }
   if (nchunks == 0)
