@@ -85,6 +85,23 @@ def test_router_logits_dense(dev, orc, T, E, K):
     _assert_logits(got, xf @ wf.T, np.abs(xf) @ np.abs(wf).T)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_router_logits_dense_random_shapes(dev, orc, seed):
+    """Seeded random token and expert counts and K (a multiple of 8, half of
+    them multiples of 128), so both kernels and both tile sizes of the tiled
+    one meet ragged edges."""
+    rng = np.random.default_rng(500 + seed)
+    T = int(rng.integers(1, 3000))
+    E = int(rng.integers(1, 600))
+    K = int(128 * rng.integers(1, 24)) if seed % 2 == 0 else int(8 * rng.integers(1, 300))
+    say(f"router logits dense random seed={seed}: T={T} E={E} K={K}")
+    x = synth.bf16_bits(rng.normal(size=(T, K)).astype(np.float32))
+    w = synth.bf16_bits((rng.normal(size=(E, K)) * 0.05).astype(np.float32))
+    got = ops.router_logits(bf16_t(x, dev), bf16_t(w, dev)).cpu().numpy()
+    xf, wf = orc.f32_from_bf16(x).astype(np.float64), orc.f32_from_bf16(w).astype(np.float64)
+    _assert_logits(got, xf @ wf.T, np.abs(xf) @ np.abs(wf).T)
+
+
 @pytest.mark.parametrize("nbits,gs", [(4, 64), (8, 64), (8, 32), (4, 128)])
 def test_router_logits_quantized(dev, orc, nbits, gs):
     say(f"router logits quantized bits={nbits} gs={gs}")
