@@ -792,7 +792,8 @@ def run_block(args, dev):
             nbytes = 256 * 2048 * 2 + 10 * (per_gu + per_dn) + 2048 * 2 * 2
             r.update(metric="HBM GB/s", value=round(nbytes / sec / 1e9, 1), bytes_per_call=nbytes,
                      pct_hbm_peak=round(100 * nbytes / sec / 1e9 / HBM_PEAK_GBS, 2),
-                     path="router + top-k + gate_up/SwiGLU GEMV + down/weighted-sum GEMV")
+                     path="router logits + gate_up/SwiGLU GEMV selecting its experts (top-k in-kernel) "
+                          "+ down/weighted-sum GEMV")
         else:
             fl = 2 * T * 10 * 2048 * 1024 + 2 * T * 10 * 512 * 2048 + 2 * T * 2048 * 256
             r.update(metric="TFLOP/s", value=round(fl / sec / 1e12, 1), flops_per_call=fl,

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 3
+#define QMOE_ABI_VERSION 4
 
 enum {
   QMOE_OK = 0,
@@ -256,6 +256,23 @@ int qmoe_moe_down_wsum_tiles(const uint16_t* h, const int32_t* idx,
                              int64_t I, const uint32_t* wp, const uint32_t* sb,
                              int32_t num_experts, int64_t D, uint16_t* y,
                              void* stream);
+
+/* qmoe_moe_gate_up_swiglu_tiles with the router's top-k folded in (replacing
+ * engine/patches/decode-fusion/fused_kernels.py:363-371 router_topk ahead of
+ * gate_up_silu, decode-fusion/kernel.py:111-138): each wave picks its pair's
+ * expert from the token's fp32 router logits [T, num_experts] by
+ * qmoe_router_topk's own selection, and the token's ids and scores (norm as
+ * in qmoe_router_topk) are written to idx and scores [T, top_k] for
+ * qmoe_moe_down_wsum_tiles, so h, idx and scores equal qmoe_router_topk
+ * followed by qmoe_moe_gate_up_swiglu_tiles, bit for bit, with one launch
+ * fewer.  Requires top_k <= 64 and num_experts <= 1024 besides the call's own
+ * envelope. */
+int qmoe_moe_gate_up_swiglu_tiles_topk(const uint16_t* x, const float* logits,
+                                       int norm, int64_t T, int64_t top_k,
+                                       int64_t K, const uint32_t* wp,
+                                       const uint32_t* sb, int32_t num_experts,
+                                       int64_t I, uint16_t* h, int32_t* idx,
+                                       float* scores, void* stream);
 
 /* ------------------------------------------------------------------ int8 --
  * int8-activation x int4-weight gate_up (replaces

@@ -263,3 +263,59 @@ def test_moe_block_resident_copies(dev, orc, resident):
     rep = orc.err_report(y, y64)
     print(f"[parity] block resident={resident}: {rep}", flush=True)
     assert rep["rel_to_max"] <= 2.0 ** -7
+
+
+def _dev_tiles(E, N, K, dev, pairs, seed):
+    """Random tile-layout weights [E, N, K] made on the device (the two paths
+    compared below read the same bytes; the values only need to be varied)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, N, K // 8), dtype=torch.int32, device=dev, generator=g)
+    s = (torch.rand(E, N, K // 64, device=dev, generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+    b = (torch.randn(E, N, K // 64, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    return ops.repack_tiles(w, s, b, swiglu_pairs=pairs)
+
+
+@pytest.mark.parametrize("T,E,k,norm", [(1, 256, 10, True), (3, 64, 8, False), (6, 300, 10, True),
+                                        (16, 32, 4, True), (2, 1024, 16, False)])
+def test_decode_topk_kernels_match_router_topk(dev, T, E, k, norm):
+    """The gate_up decode kernel that selects its own experts from the logits
+    equals router_topk followed by the id-taking kernel, bit for bit, in h and
+    in the ids and scores it hands on, on both in-kernel top-k instances
+    (E <= 256, E > 256) and with planted ties."""
+    say(f"decode top-k kernels T={T} E={E} k={k} norm={norm}")
+    K, I, D = 2048, 512, 2048
+    gu = _dev_tiles(E, 2 * I, K, dev, True, 11 + E)
+    dn = _dev_tiles(E, D, I, dev, False, 12 + E)
+    g = torch.Generator(device=dev).manual_seed(T * 131 + E)
+    x = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, device=dev, generator=g)
+    logits[:, E // 3] = logits[:, E // 5]  # ties: the lower index goes first
+    logits[0, 1] = logits[0, 0]
+    idx_ref, sc_ref = ops.router_topk(logits, k, norm)
+    h_ref = ops.gate_up_silu_tiles(x, gu, idx_ref)
+    h, idx, sc = ops.gate_up_silu_tiles_topk(x, gu, logits, k, norm)
+    y_ref = ops.down_wsum_tiles(h_ref, dn, idx_ref, sc_ref)
+    y = ops.down_wsum_tiles(h, dn, idx, sc)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, idx_ref), "ids from the gate_up kernel differ from router_topk's"
+    assert torch.equal(sc, sc_ref), "scores from the gate_up kernel differ from router_topk's"
+    assert torch.equal(h, h_ref), "gate_up from logits differs from router_topk + gate_up"
+    assert torch.equal(y, y_ref)
+
+
+def test_block_decode_takes_the_topk_kernels(dev, orc):
+    """A tile-resident block decodes through the top-k kernels, and its output
+    equals the id-taking path's."""
+    E, H, I, k = 64, 2048, 512, 10
+    gu, dn, router, _ = _block_problem(9, E, H, I)
+    blk = moe_block.SparseMoeBlock(bf16_t(router, dev), _dev_w(gu, dev), _dev_w(dn, dev), k)
+    rng = np.random.default_rng(9)
+    for T in (1, 3, 6):
+        assert blk.decodes_with_topk(T)
+        xt = bf16_t(synth.bf16_bits(rng.normal(size=(T, H)).astype(np.float32)), dev)
+        y = blk(xt)
+        idx, sc = blk.route(xt)
+        want = blk.experts(xt, idx, sc)
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), f"T={T}"
+    assert not blk.decodes_with_topk(7)  # 70 pairs: the sorted path

@@ -67,6 +67,7 @@ SIGNATURES: dict[str, tuple] = {
     "qmoe_gather_qmv_tiles": (INT, [P, P, P, I64, I64, P, P, I32, I64, P, P]),
     "qmoe_moe_gate_up_swiglu_tiles": (INT, [P, P, I64, I64, I64, P, P, I32, I64, P, P]),
     "qmoe_moe_down_wsum_tiles": (INT, [P, P, P, I64, I64, I64, P, P, I32, I64, P, P]),
+    "qmoe_moe_gate_up_swiglu_tiles_topk": (INT, [P, P, INT, I64, I64, I64, P, P, I32, I64, P, P, P, P]),
     "qmoe_quantize_act_int8": (INT, [P, I64, I64, P, P, P]),
     "qmoe_gather_qmm_int8_sorted": (INT, [P, P, P, I64, I64, P, P, P, I32, I64, INT, INT, P, P, P, P,
                                           I64, P, P]),

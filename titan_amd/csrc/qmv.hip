@@ -17,6 +17,7 @@
 #include <stdarg.h>
 
 #include "common.h"
+#include "topk.h"
 
 namespace {
 
@@ -170,7 +171,39 @@ struct QmvArgs {
   FastDiv blk_div;     // qmv64: blocks per pair
   FastDiv x_divf;      // qmv64: x_div
   float* out_f32;      // plain row form only: fp32 results here instead of bf16 in out
+  // tiled SwiGLU form: experts from each token's top-k of these [T, E] fp32
+  // logits, written with their scores to topk_idx / topk_scores [T, k]
+  const float* logits = nullptr;
+  int32_t* topk_idx = nullptr;
+  float* topk_scores = nullptr;
+  int topk_norm = 1;
 };
+
+// The expert of pair pr = t * k + j of the tiled SwiGLU form: experts[pr], or
+// with PER > 0 choice j of token t's top-k of its router logits, from the
+// first j + 1 rounds of the selection (it is greedy).  The wave of the pair's
+// first column block whose slot is the last, j = k - 1, has run all k rounds:
+// it writes the token's k ids and scores.  Wave-uniform.
+template <int PER>
+__device__ __forceinline__ int pair_expert(const QmvArgs& a, uint32_t pr, uint32_t t, bool first_block) {
+  if constexpr (PER == 0) {
+    return a.experts[pr];
+  } else {
+    const int k = (int)a.x_div;
+    const int j = __builtin_amdgcn_readfirstlane((int)(pr - t * (uint32_t)k));
+    const bool writer = first_block && j == k - 1;
+    int sel;
+    float sc;
+    qmoe_topk::wave_topk<PER>(a.logits + (int64_t)t * a.num_experts, a.num_experts, j + 1, a.topk_norm, sel, sc,
+                              writer);
+    const int lane = threadIdx.x & 63;
+    if (writer && lane < k) {
+      a.topk_idx[(int64_t)t * k + lane] = sel;
+      a.topk_scores[(int64_t)t * k + lane] = sc;
+    }
+    return __builtin_amdgcn_readlane(sel, j);
+  }
+}
 
 // MODE 0: out[r, n] = x_row . W[e][n]
 // MODE 1: out[r, i] = silu(x_row . W[e][i]) * (x_row . W[e][n_out + i])
@@ -569,21 +602,23 @@ __global__ __launch_bounds__(64) void qmv64_tiled_kernel(QmvArgs a) {
 // XCD-contiguously (xcd_item), so the row groups sharing a scale|bias chunk
 // run on one XCD.  Per lane and row the arithmetic and the reduction tree are
 // those of qmv64_kernel's fused form, so the result is bit-identical to it.
-template <int NV, int RG>
+template <int NV, int RG, int PER = 0>
 __global__ __launch_bounds__(64) void qmv64_paired_kernel(QmvArgs a) {
   static_assert(RG == 4 || RG == 8, "four or eight indices per wave");
   const int lane = threadIdx.x;
   const uint32_t item = xcd_item(blockIdx.x, gridDim.x);
   const uint32_t r = fast_div(item, a.blk_div);
   const int i0 = (int)(item - r * a.blk_div.d) * RG;
-  int e = a.experts[r];
   const uint32_t xr = fast_div(r, a.x_divf);
+  // the expert id is requested before x; a top-k selection goes after x's loads
+  int e = PER == 0 ? pair_expert<0>(a, r, xr, false) : 0;
   const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
   uint4 xa[NV][4];
 #pragma unroll
   for (int v = 0; v < NV; ++v)
 #pragma unroll
     for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q];
+  if constexpr (PER > 0) e = pair_expert<PER>(a, r, xr, i0 == 0);
   e = min(max(e, 0), a.num_experts - 1);
   const int G = 32 * NV;
   const int NC = a.n_w / 64;
@@ -669,7 +704,7 @@ __global__ __launch_bounds__(64) void qmv64_paired_kernel(QmvArgs a) {
 // nibble pairs, and the chunk's sum) and each lane reads the chunk of its
 // (g, h) per step.  Per lane the affine chunk arithmetic is qmv64_kernel's;
 // the row sums close over the eight group slots with three DPP steps.
-template <int NV, int RG>
+template <int NV, int RG, int PER = 0>
 __global__ __launch_bounds__(64) void qmv64_paired_lines_kernel(QmvArgs a) {
   static_assert(RG == 4 || RG == 8, "four or eight indices per wave");
   constexpr int NCH = 64 * NV;   // 32-element chunks of x
@@ -684,14 +719,16 @@ __global__ __launch_bounds__(64) void qmv64_paired_lines_kernel(QmvArgs a) {
   const uint32_t item = xcd_item(blockIdx.x, gridDim.x);
   const uint32_t pr = fast_div(item, a.blk_div);
   const int i0 = (int)(item - pr * a.blk_div.d) * RG;
-  int e = a.experts[pr];
   const uint32_t xr = fast_div(pr, a.x_divf);
+  // the expert id is requested before x; a top-k selection goes after x's loads
+  int e = PER == 0 ? pair_expert<0>(a, pr, xr, false) : 0;
   const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
   uint4 xa[NV][4];
 #pragma unroll
   for (int v = 0; v < NV; ++v)
 #pragma unroll
     for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q];
+  if constexpr (PER > 0) e = pair_expert<PER>(a, pr, xr, i0 == 0);
   e = min(max(e, 0), a.num_experts - 1);
   const int G = 32 * NV;
   const int NC = a.n_w / 64;
@@ -1089,7 +1126,7 @@ int launch_qmv_tiled(const QmvArgs& a, hipStream_t st) {
   return qmoe::launch_status("qmv64_tiled_kernel");
 }
 
-template <int RG>
+template <int RG, int PER = 0>
 int launch_qmv_paired_rg(QmvArgs a, hipStream_t st) {
   const int64_t nblk = a.n_out / RG;
   const int64_t blocks = a.n_pairs * nblk;
@@ -1100,12 +1137,12 @@ int launch_qmv_paired_rg(QmvArgs a, hipStream_t st) {
   a.x_divf = make_fastdiv((uint32_t)a.x_div);
   dim3 grid((unsigned)blocks), block(64);
   switch (a.K / 2048) {
-    case 1: qmv64_paired_kernel<1, RG><<<grid, block, 0, st>>>(a); break;
-    case 2: qmv64_paired_kernel<2, RG><<<grid, block, 0, st>>>(a); break;
+    case 1: qmv64_paired_kernel<1, RG, PER><<<grid, block, 0, st>>>(a); break;
+    case 2: qmv64_paired_kernel<2, RG, PER><<<grid, block, 0, st>>>(a); break;
     default:
       if constexpr (RG == 4) {
-        if (a.K / 2048 == 3) qmv64_paired_kernel<3, 4><<<grid, block, 0, st>>>(a);
-        else qmv64_paired_kernel<4, 4><<<grid, block, 0, st>>>(a);
+        if (a.K / 2048 == 3) qmv64_paired_kernel<3, 4, PER><<<grid, block, 0, st>>>(a);
+        else qmv64_paired_kernel<4, 4, PER><<<grid, block, 0, st>>>(a);
       } else {
         return qmoe::fail(QMOE_ERR_UNSUPPORTED, "K=%d: %d indices per wave take K <= 4096", a.K, RG);
       }
@@ -1122,6 +1159,7 @@ int launch_qmv_paired_rg(QmvArgs a, hipStream_t st) {
 #define QMOE_PAIRED_LINES_RG 4
 #endif
 
+template <int PER = 0>
 int launch_qmv_paired(const QmvArgs& a, hipStream_t st) {
   if (a.K <= 4096) {
     // line reads with x staged in LDS (K = 2048 or 4096)
@@ -1135,11 +1173,11 @@ int launch_qmv_paired(const QmvArgs& a, hipStream_t st) {
     b.blk_div = make_fastdiv((uint32_t)nblk);
     b.x_divf = make_fastdiv((uint32_t)a.x_div);
     dim3 grid((unsigned)blocks), block(64);
-    if (a.K == 2048) qmv64_paired_lines_kernel<1, RG><<<grid, block, 0, st>>>(b);
-    else qmv64_paired_lines_kernel<2, RG><<<grid, block, 0, st>>>(b);
+    if (a.K == 2048) qmv64_paired_lines_kernel<1, RG, PER><<<grid, block, 0, st>>>(b);
+    else qmv64_paired_lines_kernel<2, RG, PER><<<grid, block, 0, st>>>(b);
     return qmoe::launch_status("qmv64_paired_lines_kernel");
   }
-  return launch_qmv_paired_rg<4>(a, st);
+  return launch_qmv_paired_rg<4, PER>(a, st);
 }
 
 int check_tiled(int64_t K, int64_t rows_per_expert, const void* x, const void* wp, const void* sb) {
@@ -1327,6 +1365,44 @@ extern "C" int qmoe_moe_down_wsum_tiles(const uint16_t* h, const int32_t* idx, c
   if (R == 8) down_pair_tiled_kernel<8><<<grid, block, 0, st>>>(a);
   else down_pair_tiled_kernel<16><<<grid, block, 0, st>>>(a);
   return qmoe::launch_status("down_pair_tiled_kernel");
+}
+
+namespace {
+// Routing from logits: k <= 64 choices of at most 1024 experts (the router
+// top-k's envelope), four or sixteen logits per lane.
+int check_topk(const float* logits, int64_t top_k, int32_t num_experts, int* per) {
+  if (!logits) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  if (top_k > num_experts)
+    return qmoe::fail(QMOE_ERR_INVALID, "top_k=%lld > num_experts=%d", (long long)top_k, num_experts);
+  if (top_k > qmoe_topk::kMaxK || num_experts > 64 * qmoe_topk::kMaxPer)
+    return qmoe::fail(QMOE_ERR_UNSUPPORTED, "top_k=%lld, E=%d: the in-kernel top-k takes k <= %d, E <= %d",
+                      (long long)top_k, num_experts, qmoe_topk::kMaxK, 64 * qmoe_topk::kMaxPer);
+  *per = num_experts <= 256 ? 4 : 16;
+  return QMOE_OK;
+}
+}  // namespace
+
+extern "C" int qmoe_moe_gate_up_swiglu_tiles_topk(const uint16_t* x, const float* logits, int norm, int64_t T,
+                                                  int64_t top_k, int64_t K, const uint32_t* wp, const uint32_t* sb,
+                                                  int32_t num_experts, int64_t I, uint16_t* h, int32_t* idx,
+                                                  float* scores, void* stream) {
+  if (T < 0 || top_k <= 0 || I <= 0 || num_experts <= 0) return qmoe::fail(QMOE_ERR_INVALID, "bad sizes");
+  if (T == 0) return QMOE_OK;
+  if (!x || !wp || !sb || !h || !idx || !scores) return qmoe::fail(QMOE_ERR_INVALID, "null pointer");
+  int per = 0;
+  int rc = check_topk(logits, top_k, num_experts, &per);
+  if (rc) return rc;
+  if (I % 32) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "I=%lld: the paired layout needs I %% 32 == 0", (long long)I);
+  rc = check_tiled(K, 2 * I, x, wp, sb);
+  if (rc) return rc;
+  QmvArgs a{x, K, nullptr, top_k, nullptr, T * top_k, (int)K, 64, wp, nullptr, nullptr, num_experts, (int)I,
+            (int)(2 * I), h, sb};
+  a.logits = logits;
+  a.topk_idx = idx;
+  a.topk_scores = scores;
+  a.topk_norm = norm ? 1 : 0;
+  hipStream_t st = qmoe::as_stream(stream);
+  return per == 4 ? launch_qmv_paired<4>(a, st) : launch_qmv_paired<16>(a, st);
 }
 
 #ifdef QMOE_QMV_STAMPS

@@ -1,60 +1,18 @@
-// Router top-k over fp32 logits, one wave per token (gfx950).
-//
-// Semantics: the reference's fused router
-// (engine/patches/decode-fusion/fused_kernels.py:288-330 kernel source,
-// :363-371 router_topk): the k largest logits in descending order, ties to
-// the lower expert index, and the scores
-//   norm:  exp(l_j - l_0) / sum_{j<k} exp(l_j - l_0)   -- softmax renormalised
-//          over the chosen experts (qwen3_5_moe/language.py:65-71);
-//   else:  exp(l_j - max) / sum_e exp(l_e - max)        -- the full softmax.
-// Softmax is monotonic, so selecting on logits selects the same experts as
-// selecting on softmax probabilities, without rounding them to bf16 first
-// (the stock path's bf16 gates can tie where the logits do not).
-//
-// Lane l holds experts l, l + 64, ... (PER per lane, coalesced loads).  Each
-// round takes the wave maximum of the lanes' best untaken values, then the
-// lowest expert index holding it (one ballot per column of 64 experts), and
-// retires that expert in its owner lane.
+// Router top-k over fp32 logits, one wave per token, and the router logits
+// (gfx950).  The selection itself (semantics, tie order, scores) is
+// qmoe_topk::wave_topk in topk.h, which the decode kernels that pick their own
+// experts share.
 #include <limits.h>
 
 #include "common.h"
 #include "gemm_common.h"
+#include "topk.h"
 
 namespace {
 
-constexpr int kMaxK = 64;
-constexpr int kMaxPer = 16;  // E <= 1024
-
-// Whole-wave reductions that leave the result in every lane, without the
-// LDS crossbar (__shfl_xor lowers to ds_bpermute, whose latency dominated a
-// k-round top-k): two quad_perm steps, row_half_mirror and row_ror:8 cover a
-// 16-lane row with DPP, then v_permlane16_swap and v_permlane32_swap combine
-// the rows.
-template <class Op>
-__device__ __forceinline__ float wave_all(float v, Op op) {
-  auto dpp = [](float x, int ctrl) {
-    switch (ctrl) {  // the control word must be a constant
-      case 0xB1: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0xB1, 0xf, 0xf, false));
-      case 0x4E: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x4E, 0xf, 0xf, false));
-      case 0x141: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x141, 0xf, 0xf, false));
-      default: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x128, 0xf, 0xf, false));
-    }
-  };
-  v = op(v, dpp(v, 0xB1));   // quad_perm 1,0,3,2
-  v = op(v, dpp(v, 0x4E));   // quad_perm 2,3,0,1
-  v = op(v, dpp(v, 0x141));  // row_half_mirror
-  v = op(v, dpp(v, 0x128));  // row_ror:8
-  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = op(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return op(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-}
-__device__ __forceinline__ float wave_max(float v) {
-  return wave_all(v, [](float a, float b) { return fmaxf(a, b); });
-}
-__device__ __forceinline__ float wave_sum(float v) {
-  return wave_all(v, [](float a, float b) { return a + b; });
-}
+using qmoe_topk::kMaxK;
+using qmoe_topk::kMaxPer;
+using qmoe_topk::wave_sum;
 
 template <int PER>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int64_t T, int E, int k,
@@ -63,57 +21,12 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
   const int64_t t = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
   if (t >= T) return;
-  const float* lp = logits + t * E;
-  float v[PER];
-  uint32_t taken = 0;  // bit c: expert c * 64 + lane already chosen (or absent)
-#pragma unroll
-  for (int c = 0; c < PER; ++c) {
-    const int e = c * 64 + lane;
-    v[c] = e < E ? lp[e] : -INFINITY;
-    if (e >= E) taken |= 1u << c;
-  }
-  float lmax = -INFINITY;
-#pragma unroll
-  for (int c = 0; c < PER; ++c)
-    if (!(taken >> c & 1)) lmax = fmaxf(lmax, v[c]);
-  const float gmax = wave_max(lmax);
-  float all = 0.f;  // sum over every expert of exp(l - max), for the full softmax
-  if (!norm) {
-#pragma unroll
-    for (int c = 0; c < PER; ++c)
-      if (!(taken >> c & 1)) all += expf(v[c] - gmax);
-    all = wave_sum(all);
-  }
-
-  float mine = -INFINITY;  // lane j keeps the j-th chosen logit
-  for (int j = 0; j < k; ++j) {
-    float bv = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < PER; ++c)
-      if (!(taken >> c & 1)) bv = fmaxf(bv, v[c]);
-    const float wm = wave_max(bv);
-    // the lowest expert index holding the maximum: column c = e / 64 first,
-    // then the lowest lane of that column (one ballot per column)
-    int sel = 0;  // no comparable candidate (NaN logits): stay in range
-#pragma unroll
-    for (int c = 0; c < PER; ++c) {
-      const uint64_t m = __ballot(!(taken >> c & 1) && v[c] == wm);
-      if (m) {
-        sel = 64 * c + __builtin_ctzll(m);
-        break;
-      }
-    }
-    if (lane == (sel & 63)) taken |= 1u << (sel >> 6);
-    if (lane == 0) idx[t * k + j] = sel;
-    if (lane == j) mine = wm;
-  }
-  if (norm) {
-    const float top0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(mine), 0));
-    const float p = lane < k ? expf(mine - top0) : 0.f;
-    const float denom = wave_sum(p);
-    if (lane < k) scores[t * k + lane] = p / denom;
-  } else {
-    if (lane < k) scores[t * k + lane] = expf(mine - gmax) / all;
+  int sel;
+  float sc;
+  qmoe_topk::wave_topk<PER>(logits + t * E, E, k, norm, sel, sc);
+  if (lane < k) {
+    idx[t * k + lane] = sel;
+    scores[t * k + lane] = sc;
   }
 }
 

@@ -7,8 +7,11 @@ engine/patches/decode-fusion/fused_kernels.py:232-371).
                                                      T <= 16), else qmoe_router_logits_dense
     idx, sc = top-k of logits, softmax over the k    qmoe_router_topk
     decode  (T * k < 64, switch_layers.py:218):
-        h   = silu(x W_gate^T) * (x W_up^T)          qmoe_moe_gate_up_swiglu_tiles
+        h   = silu(x W_gate^T) * (x W_up^T)          qmoe_moe_gate_up_swiglu_tiles[_topk]
         y   = sum_j sc_j * W_down[idx_j] h_j          qmoe_moe_down_wsum_tiles
+        (the _topk form selects idx and sc from the logits in-kernel, by the
+        top-k's own code, and writes them for the down kernel, so the decode
+        block is three launches)
     prefill:
         order, tiles = stable sort of the pairs       qmoe_route
         h   = SwiGLU gate_up grouped GEMM             qmoe_gather_qmm_swiglu_sorted_tiles
@@ -207,11 +210,24 @@ class SparseMoeBlock:
         z = ops.router_logits(x2, sh.gate_weight)
         return (torch.sigmoid(z) * y.float()).to(torch.bfloat16)
 
+    def decodes_with_topk(self, T: int) -> bool:
+        """Does a call with T tokens take the gate_up decode kernel that picks
+        its experts from the router logits itself and hands the ids and scores
+        to the down kernel (qmoe_moe_gate_up_swiglu_tiles_topk: one launch
+        fewer than router_topk + the decode kernels, same results)?"""
+        return (self.decode_tiles and T <= 16 and T * self.top_k < self.sort_min_pairs
+                and self.top_k <= 16 and self.num_experts <= 1024)
+
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         H = x.shape[-1]
         x2 = x.reshape(-1, H).to(torch.bfloat16).contiguous()
-        idx, scores = self.route(x2)
-        y = self.experts(x2, idx, scores)
+        if self.decodes_with_topk(x2.shape[0]):
+            h, idx, scores = ops.gate_up_silu_tiles_topk(x2, self.gu_tiles, self.route_logits(x2), self.top_k,
+                                                         self.norm)
+            y = ops.down_wsum_tiles(h, self.down_tiles, idx, scores)
+        else:
+            idx, scores = self.route(x2)
+            y = self.experts(x2, idx, scores)
         if self.shared is not None:
             y = (y.float() + self.shared_expert(x2).float()).to(torch.bfloat16)
         return y.reshape(x.shape)

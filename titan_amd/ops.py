@@ -380,6 +380,37 @@ def down_wsum_tiles(h: torch.Tensor, tw: TileWeights, idx: torch.Tensor, scores:
     return y
 
 
+def _logits(logits: torch.Tensor, T: int, E: int, device) -> torch.Tensor:
+    lg = _f32(logits, "logits", device)
+    if tuple(lg.shape) != (T, E):
+        raise ValueError(f"logits must be [T, E] = [{T}, {E}], got {tuple(lg.shape)}")
+    return lg
+
+
+def gate_up_silu_tiles_topk(x: torch.Tensor, tw: TileWeights, logits: torch.Tensor, top_k: int,
+                            norm: bool = True):
+    """:func:`gate_up_silu_tiles` with each token's experts chosen in the kernel
+    from its fp32 router logits [T, E] by :func:`router_topk`'s selection.
+    Returns (h [T, k, I], idx int32 [T, k], scores fp32 [T, k]), equal to
+    ``idx, scores = router_topk(logits, top_k, norm)`` and
+    ``h = gate_up_silu_tiles(x, tw, idx)``, with one launch fewer."""
+    if not tw.swiglu_pairs:
+        raise ValueError("the decode SwiGLU kernel needs weights repacked with swiglu_pairs=True")
+    x = _bf16(x, "x")
+    T, K = x.shape
+    if K != tw.K:
+        raise ValueError(f"x has K={K}, the weights K={tw.K}")
+    lg = _logits(logits, T, tw.num_experts, x.device)
+    I = tw.N // 2
+    h = torch.empty(T, top_k, I, dtype=torch.bfloat16, device=x.device)
+    idx = torch.empty(T, top_k, dtype=torch.int32, device=x.device)
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
+    _lib.call("qmoe_moe_gate_up_swiglu_tiles_topk", x.data_ptr(), lg.data_ptr(), int(bool(norm)), T, top_k, K,
+              tw.wp.data_ptr(), tw.sb.data_ptr(), tw.num_experts, I, h.data_ptr(), idx.data_ptr(),
+              scores.data_ptr(), _stream(x))
+    return h, idx, scores
+
+
 def gemm_supported(K: int, N: int, group_size: int, bits: int) -> bool:
     return bits == 4 and group_size == 64 and K % 128 == 0 and N % 256 == 0
 
@@ -655,7 +686,7 @@ def router_logits(x: torch.Tensor, router, group_size: int = GROUP, bits: int = 
 __all__ = [
     "GROUP", "BITS", "QmoeError", "QmoeUnsupported", "TileTable", "TileWeights", "Routing", "build_tiles", "route",
     "repack_tiles", "gather_qmm_sorted_tiles", "gather_qmm_int8_sorted_tiles", "router_topk", "router_logits", "gather_qmm_swiglu_sorted_tiles", "swiglu_pair_order", "gather_qmv_tiles", "gate_up_silu_tiles",
-    "down_wsum_tiles",
+    "down_wsum_tiles", "gate_up_silu_tiles_topk",
     "max_tiles", "tile_rows", "unpack", "dequantize", "gather_qmv", "gather_qmm_sorted", "gather_qmm",
     "gemm_supported", "quantized_matmul", "gate_up_silu", "down_wsum", "moe_weighted_sum",
     "quantize_act_int8", "gather_qmm_int8_sorted",
