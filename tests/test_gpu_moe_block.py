@@ -53,6 +53,34 @@ def test_router_topk_ties_take_lower_index(dev, orc):
     np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("E", [100, 600])
+def test_router_topk_nan_logits_rank_last(dev, E):
+    """Logits are expected finite; a NaN ranks below every number: the
+    choices are the finite logits in descending order (ties to the lower
+    index), then the NaN entries in index order, and -0 ties with +0.  Pinned
+    against a numpy sort of (-value, index) with NaN mapped below -inf."""
+    say(f"router top-k with NaN logits E={E}")
+    rng = np.random.default_rng(E)
+    T, k = 3, 16
+    lg = rng.normal(size=(T, E)).astype(np.float32)
+    lg[0, [5, 17, 63]] = np.nan
+    lg[1, :] = np.nan
+    lg[1, [9, 2, 70]] = [1.0, 3.0, -np.inf]  # three numbers, then NaN in index order
+    lg[2, :] = -np.abs(lg[2, :]) - 1.0
+    lg[2, [8, 4]] = [-0.0, 0.0]  # signed zeros tie: index 4 first
+    lg[2, [1, 3]] = [7.0, 7.0]
+    idx, sc = ops.router_topk(f32_t(lg, dev), k, True)
+    idx = idx.cpu().numpy()
+    for t in range(T):
+        v = lg[t].astype(np.float64)
+        rank = np.where(np.isnan(v), -np.inf, v)
+        order = np.lexsort((np.arange(E), np.isnan(v), -rank))  # finite first by value, NaN after, then index
+        assert idx[t].tolist() == order[:k].tolist(), t
+    assert idx[1, :3].tolist() == [2, 9, 70] and idx[1, 3:6].tolist() == [0, 1, 3]
+    assert idx[2, :4].tolist() == [1, 3, 4, 8]
+    assert np.all(np.isfinite(sc.cpu().numpy()[[0, 2]]))
+
+
 def _assert_logits(got, ref64, absx_absw):
     """fp32 accumulation bound: |got - ref| <= 2^-14 * sum_k |x_k||w_k| per
     element, i.e. n * 2^-24 for n = 1024 sequential roundings.  The GEMV
