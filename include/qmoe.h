@@ -336,7 +336,8 @@ int qmoe_gather_qmm_swiglu_sorted_tiles(const uint16_t* x, const int32_t* x_rows
  * renormalise of qwen3_5_moe/language.py:65-71): idx[t, j] the j-th largest
  * logit's expert (descending, ties to the lower index), scores[t, j] fp32:
  * norm != 0: exp(l_j - l_0) / sum_{j<k} exp(l_j - l_0); norm == 0: the full
- * softmax probability.  k <= 64, E <= 1024; logits are expected finite. */
+ * softmax probability.  k <= 64, E <= 1024; logits are expected finite (a
+ * NaN ranks below every number, after which ties go to the lower index). */
 int qmoe_router_topk(const float* logits, int64_t T, int64_t E, int64_t k,
                      int norm, int32_t* idx, float* scores, void* stream);
 
