@@ -303,15 +303,17 @@ def _dev_tiles(E, N, K, dev, pairs, seed):
     return ops.repack_tiles(w, s, b, swiglu_pairs=pairs)
 
 
-@pytest.mark.parametrize("T,E,k,norm", [(1, 256, 10, True), (3, 64, 8, False), (6, 300, 10, True),
-                                        (16, 32, 4, True), (2, 1024, 16, False)])
-def test_decode_topk_kernels_match_router_topk(dev, T, E, k, norm):
+@pytest.mark.parametrize("T,E,k,norm,K", [(1, 256, 10, True, 2048), (3, 64, 8, False, 2048),
+                                          (6, 300, 10, True, 4096), (16, 32, 4, True, 2048),
+                                          (2, 1024, 16, False, 2048), (1, 256, 10, True, 6144),
+                                          (4, 128, 8, False, 8192)])
+def test_decode_topk_kernels_match_router_topk(dev, T, E, k, norm, K):
     """The gate_up decode kernel that selects its own experts from the logits
     equals router_topk followed by the id-taking kernel, bit for bit, in h and
     in the ids and scores it hands on, on both in-kernel top-k instances
     (E <= 256, E > 256) and with planted ties."""
-    say(f"decode top-k kernels T={T} E={E} k={k} norm={norm}")
-    K, I, D = 2048, 512, 2048
+    say(f"decode top-k kernels T={T} E={E} k={k} norm={norm} K={K}")
+    I, D = 512, K
     gu = _dev_tiles(E, 2 * I, K, dev, True, 11 + E)
     dn = _dev_tiles(E, D, I, dev, False, 12 + E)
     g = torch.Generator(device=dev).manual_seed(T * 131 + E)
