@@ -952,8 +952,14 @@ __global__ __launch_bounds__(64 * kPairMaxK) void down_pair_kernel(DownArgs a) {
 // consecutive rows (64 contiguous bytes per (g, h)); the R rows of a wave
 // (d0 % R == 0, R | 32) fill whole 128-byte lines across its R/4 loads, which
 // are ordinary (cached) loads so the later ones find the lines the first ones
-// brought in.  The rows' scale|bias words are 4-byte loads from the group's
-// 256-byte chunk.  (Eight lanes per line with two h chunks per lane measured
+// brought in.  The wave's scale|bias words (R per group, consecutive in the
+// group's 256-byte chunk) arrive in one coalesced load and are moved to the
+// lanes that need them across rows: with R = 16, lane row rg loads words
+// 4rg..4rg+3 and two permlane32 and two permlane16 swaps transpose that 4 x 4
+// block so VGPR i holds word 4i + rg; with R = 8, lane (rg, h) loads word
+// rg + 4h and swaps it with its h neighbour.  (Four scattered 4-byte loads per
+// wave instead, each touching eight chunks, cost 17-23% of the kernel at 8
+// and 16 tokens.  Eight lanes per line with two h chunks per lane measured
 // slower: every wave then reads twice the h row.)
 template <int R>
 __global__ __launch_bounds__(64 * kPairMaxK) void down_pair_tiled_kernel(DownArgs a) {
@@ -973,14 +979,35 @@ __global__ __launch_bounds__(64 * kPairMaxK) void down_pair_tiled_kernel(DownArg
   int e = a.idx[p];
   e = min(max(e, 0), a.num_experts - 1);
   const float sc = a.scores[p];
+  static_assert(R == 8 || R == 16, "rows per wave");
+  // D % 64 == 0 and d0 % R == 0: the wave's rows lie in one 64-row chunk
+  const int64_t chunk = ((int64_t)e * NCd + (d0 >> 6)) * 8 + g;
+  const uint32_t* sbg = a.sb + chunk * 64 + (d0 & 63);
+  uint4 sq;
+  uint32_t s1;
+  if constexpr (NI == 4) sq = *reinterpret_cast<const uint4*>(sbg + 4 * rg);
+  else s1 = sbg[rg + 4 * h];
   uint4 wq[NI];
-  uint32_t sbw[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const int row = min(d0 + 4 * i + rg, D - 1);
-    const int64_t chunk = ((int64_t)e * NCd + (row >> 6)) * 8 + g;
+    const int row = d0 + 4 * i + rg;
     wq[i] = *(reinterpret_cast<const uint4*>(a.w) + ((chunk * 2 + ((row >> 5) & 1)) * 2 + h) * 32 + (row & 31));
-    sbw[i] = a.sb[chunk * 64 + (row & 63)];
+  }
+  uint32_t sbw[NI];  // the scale|bias word of row d0 + 4i + rg, group g
+  if constexpr (NI == 4) {
+    // lane row r holds M[r][c] = word 4r + c; after the swaps VGPR i holds M[i][r]
+    const auto x02 = __builtin_amdgcn_permlane32_swap(sq.x, sq.z, false, false);  // rows 2,3 of c0/c1 <-> rows 0,1 of c2/c3
+    const auto x13 = __builtin_amdgcn_permlane32_swap(sq.y, sq.w, false, false);
+    const auto y01 = __builtin_amdgcn_permlane16_swap(x02[0], x13[0], false, false);  // odd rows <-> even rows
+    const auto y23 = __builtin_amdgcn_permlane16_swap(x02[1], x13[1], false, false);
+    sbw[0] = y01[0];
+    sbw[1] = y01[1];
+    sbw[2] = y23[0];
+    sbw[3] = y23[1];
+  } else {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)s1, 0xB1, 0xf, 0xf, false);  // lane ^ 1
+    sbw[0] = h ? o : s1;
+    sbw[1] = h ? s1 : o;
   }
   const uint32_t mv = magic_vgpr();
 #pragma unroll
