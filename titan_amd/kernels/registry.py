@@ -169,7 +169,7 @@ class KernelRegistry:
         try:
             return self._ops[name]
         except KeyError:
-            raise ConfigError(f"no such op {name!r}; registered: {', '.join(self.names())}") from None
+            raise ConfigError(f"unknown kernel op {name!r} (known ops: {', '.join(self.names())})") from None
 
     def names(self) -> tuple[str, ...]:
         return tuple(sorted({op.name for op in self._ops.values()}))
@@ -178,7 +178,7 @@ class KernelRegistry:
         """Reject a configuration naming an op that does not exist (registry.py:209-216)."""
         for name in (*self.config.disabled, *self.config.enabled, *self.config.prefill_only):
             if name not in self._ops:
-                raise ConfigError(f"kernels config names {name!r}, which is not a registered op")
+                raise ConfigError(f"the kernel configuration lists {name!r}, but no op of that name exists")
 
     def _fast_allowed(self, op: KernelOp) -> bool:
         """registry.py:219-243: disabled wins, ``enabled`` is an allowlist,
@@ -241,7 +241,7 @@ class KernelRegistry:
             self._fast_calls[op.name] = self._fast_calls.get(op.name, 0) + 1
             return out
 
-        dispatch.__name__ = f"titan_kernel_{op.name}"
+        dispatch.__name__ = f"qmoe_dispatch_{op.name}"
         dispatch.__doc__ = op.reference_fn.__doc__
         return dispatch
 
