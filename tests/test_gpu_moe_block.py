@@ -53,6 +53,23 @@ def test_router_topk_ties_take_lower_index(dev, orc):
     np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("E,k", [(64, 64), (100, 33), (256, 10), (256, 64), (512, 8), (1024, 64)])
+def test_router_topk_many_ties(dev, orc, E, k):
+    """Logits drawn from seven values (and signed zeros), so most rounds pick
+    among equal logits held by several lanes and columns: ties go to the
+    lower expert index."""
+    say(f"router top-k, many ties, E={E} k={k}")
+    rng = np.random.default_rng(E * 131 + k)
+    T = 64
+    lg = rng.integers(-3, 4, size=(T, E)).astype(np.float32)
+    lg[T // 2:] = np.where(rng.random((T - T // 2, E)) < 0.5, -0.0, 0.0).astype(np.float32)
+    for norm in (True, False):
+        idx, sc = ops.router_topk(f32_t(lg, dev), k, norm)
+        ridx, rsc = orc.router_topk(lg, k, norm)
+        assert np.array_equal(idx.cpu().numpy(), ridx)
+        np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
+
+
 @pytest.mark.parametrize("E", [100, 600])
 def test_router_topk_nan_logits_rank_last(dev, E):
     """Logits are expected finite; a NaN ranks below every number: the
@@ -331,6 +348,27 @@ def test_decode_topk_kernels_match_router_topk(dev, T, E, k, norm, K):
     assert torch.equal(sc, sc_ref), "scores from the gate_up kernel differ from router_topk's"
     assert torch.equal(h, h_ref), "gate_up from logits differs from router_topk + gate_up"
     assert torch.equal(y, y_ref)
+
+
+@pytest.mark.parametrize("E,k", [(256, 10), (1024, 16)])
+def test_decode_topk_kernels_many_ties(dev, orc, E, k):
+    """As above with logits from five values, so most choices are decided by
+    the index: every wave's own choice (h), the written ids and the router
+    top-k agree with the oracle's ids."""
+    say(f"decode top-k kernels, many ties, E={E} k={k}")
+    T, K, I = 4, 2048, 512
+    gu = _dev_tiles(E, 2 * I, K, dev, True, 21 + E)
+    rng = np.random.default_rng(E + k)
+    lg = rng.integers(-2, 3, size=(T, E)).astype(np.float32)
+    logits = f32_t(lg, dev)
+    x = torch.randn(T, K, device=dev, generator=torch.Generator(device=dev).manual_seed(E)).to(torch.bfloat16)
+    ridx, rsc = orc.router_topk(lg, k, True)
+    h, idx, sc = ops.gate_up_silu_tiles_topk(x, gu, logits, k, True)
+    h_ref = ops.gate_up_silu_tiles(x, gu, torch.from_numpy(ridx).to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(sc.cpu().numpy(), rsc, rtol=4e-6, atol=1e-7)
+    assert torch.equal(h, h_ref)
 
 
 def test_block_decode_takes_the_topk_kernels(dev, orc):

@@ -180,28 +180,47 @@ struct QmvArgs {
 };
 
 // The expert of pair pr = t * k + j of the tiled SwiGLU form: experts[pr], or
-// with PER > 0 choice j of token t's top-k of its router logits, from the
-// first j + 1 rounds of the selection (it is greedy).  The wave of the pair's
-// first column block whose slot is the last, j = k - 1, has run all k rounds:
-// it writes the token's k ids and scores.  Wave-uniform.
+// with PER > 0 choice j of token t's top-k of its router logits, which is the
+// last choice of its top-(j + 1) (the order is by value, then index).  The
+// wave of the token's first column block and last slot, j = k - 1, also
+// writes the token's k ids and scores: it runs the whole selection here, keeps
+// it in ts, and computes and stores the scores in pair_topk_store, which the
+// kernel calls once its weight loads are in flight.  Wave-uniform.
 template <int PER>
-__device__ __forceinline__ int pair_expert(const QmvArgs& a, uint32_t pr, uint32_t t, bool first_block) {
+struct PairTopk {
+  bool writer = false;
+  float v[PER > 0 ? PER : 1];
+  int idx = 0;
+  uint32_t key_j = 0;
+};
+
+template <int PER>
+__device__ __forceinline__ int pair_expert(const QmvArgs& a, uint32_t pr, uint32_t t, bool first_block,
+                                           PairTopk<PER>& ts) {
   if constexpr (PER == 0) {
     return a.experts[pr];
   } else {
     const int k = (int)a.x_div;
     const int j = __builtin_amdgcn_readfirstlane((int)(pr - t * (uint32_t)k));
-    const bool writer = first_block && j == k - 1;
-    int sel;
-    float sc;
-    qmoe_topk::wave_topk<PER>(a.logits + (int64_t)t * a.num_experts, a.num_experts, j + 1, a.topk_norm, sel, sc,
-                              writer);
+    const float* lp = a.logits + (int64_t)t * a.num_experts;
+    ts.writer = first_block && j == k - 1;
+    if (!ts.writer) return qmoe_topk::wave_topk_last<PER>(lp, a.num_experts, j + 1);
+    qmoe_topk::wave_topk_select<PER>(lp, a.num_experts, k, ts.v, ts.idx, ts.key_j);
+    return __builtin_amdgcn_readlane(ts.idx, j);
+  }
+}
+
+template <int PER>
+__device__ __forceinline__ void pair_topk_store(const QmvArgs& a, uint32_t t, const PairTopk<PER>& ts) {
+  if constexpr (PER > 0) {
+    if (!ts.writer) return;
+    const int k = (int)a.x_div;
+    const float sc = qmoe_topk::wave_topk_scores<PER>(ts.v, k, a.topk_norm, ts.key_j);
     const int lane = threadIdx.x & 63;
-    if (writer && lane < k) {
-      a.topk_idx[(int64_t)t * k + lane] = sel;
+    if (lane < k) {
+      a.topk_idx[(int64_t)t * k + lane] = ts.idx;
       a.topk_scores[(int64_t)t * k + lane] = sc;
     }
-    return __builtin_amdgcn_readlane(sel, j);
   }
 }
 
@@ -611,14 +630,16 @@ __global__ __launch_bounds__(64) void qmv64_paired_kernel(QmvArgs a) {
   const int i0 = (int)(item - r * a.blk_div.d) * RG;
   const uint32_t xr = fast_div(r, a.x_divf);
   // the expert id is requested before x; a top-k selection goes after x's loads
-  int e = PER == 0 ? pair_expert<0>(a, r, xr, false) : 0;
+  PairTopk<PER> ts;
+  int e = 0;
+  if constexpr (PER == 0) e = pair_expert<PER>(a, r, xr, false, ts);
   const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
   uint4 xa[NV][4];
 #pragma unroll
   for (int v = 0; v < NV; ++v)
 #pragma unroll
     for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q];
-  if constexpr (PER > 0) e = pair_expert<PER>(a, r, xr, i0 == 0);
+  if constexpr (PER > 0) e = pair_expert<PER>(a, r, xr, i0 == 0, ts);
   e = min(max(e, 0), a.num_experts - 1);
   const int G = 32 * NV;
   const int NC = a.n_w / 64;
@@ -645,6 +666,7 @@ __global__ __launch_bounds__(64) void qmv64_paired_kernel(QmvArgs a) {
       wg[q][v] = load_nt(units);       // half j = 0: gate
       wu[q][v] = load_nt(units + 64);  // half j = 1: up, two 32-unit halves further
     }
+  pair_topk_store<PER>(a, xr, ts);  // while the weights are in flight
   XChunk xc[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -721,14 +743,16 @@ __global__ __launch_bounds__(64) void qmv64_paired_lines_kernel(QmvArgs a) {
   const int i0 = (int)(item - pr * a.blk_div.d) * RG;
   const uint32_t xr = fast_div(pr, a.x_divf);
   // the expert id is requested before x; a top-k selection goes after x's loads
-  int e = PER == 0 ? pair_expert<0>(a, pr, xr, false) : 0;
+  PairTopk<PER> ts;
+  int e = 0;
+  if constexpr (PER == 0) e = pair_expert<PER>(a, pr, xr, false, ts);
   const uint16_t* xrow = a.x + (int64_t)xr * a.x_stride;
   uint4 xa[NV][4];
 #pragma unroll
   for (int v = 0; v < NV; ++v)
 #pragma unroll
     for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(xrow + v * 2048 + lane * 32)[q];
-  if constexpr (PER > 0) e = pair_expert<PER>(a, pr, xr, i0 == 0);
+  if constexpr (PER > 0) e = pair_expert<PER>(a, pr, xr, i0 == 0, ts);
   e = min(max(e, 0), a.num_experts - 1);
   const int G = 32 * NV;
   const int NC = a.n_w / 64;
@@ -752,6 +776,7 @@ __global__ __launch_bounds__(64) void qmv64_paired_lines_kernel(QmvArgs a) {
         const int64_t chunk = cbase + 8 * pp + sl;
         wv[pp][h][jj] = load_nt(reinterpret_cast<const uint4*>(a.w) + ((chunk * 2 + jr + jj) * 2 + h) * 32 + l0 + rr);
       }
+  pair_topk_store<PER>(a, xr, ts);  // while the weights are in flight
   // stage x: lane l writes chunk v*64 + l (elements v*2048 + 32l ..)
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
