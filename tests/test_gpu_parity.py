@@ -582,12 +582,30 @@ def test_gather_qmv_bits_and_groups(dev, orc, nbits, gs):
     assert np.array_equal(bits(yg).reshape(R, N), bits(y))
 
 
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("M,K", [(1, 6144), (3, 8192)])
+def test_8bit_fast_gemv_wide_k(dev, orc, gs, M, K):
+    """8-bit codes at K = 2048 * n beyond the lane split's reach (K > 4096) run
+    on the 2048-chunk GEMV."""
+    say(f"8-bit quantized_matmul gs={gs} M={M} K={K}")
+    rng = np.random.default_rng(K + gs + M)
+    N = 96
+    w, s, b = synth.quant_weights(rng, (N,), K, group_size=gs, bits=8)
+    x = synth.bf16_bits(rng.normal(size=(M, K)).astype(np.float32))
+    y = ops.quantized_matmul(bf16_t(x, dev), words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), group_size=gs,
+                             bits=8)
+    ref64, _ = orc.gather_qmm_rows(x, None, np.zeros(M, np.int32), w[None], s[None], b[None], group_size=gs,
+                                   bits=8)
+    assert_close_bf16(orc, bits(y), ref64, what=f"qmm8 gs{gs} {M}x{N}x{K}")
+
+
 def test_8bit_unsupported_shapes_are_declined(dev):
-    """8-bit codes need a lane split (K <= 4096); the fused decode kernels take 4-bit only."""
+    """8-bit codes take K = 2048 * n (n <= 4) or a lane split (K <= 4096); the
+    fused decode kernels take 4-bit only."""
     say("8-bit declines")
     rng = np.random.default_rng(5)
-    w, s, b = synth.quant_weights(rng, (64,), 8192, bits=8)
-    x = bf16_t(synth.bf16_bits(rng.normal(size=(1, 8192)).astype(np.float32)), dev)
+    w, s, b = synth.quant_weights(rng, (64,), 10240, bits=8)
+    x = bf16_t(synth.bf16_bits(rng.normal(size=(1, 10240)).astype(np.float32)), dev)
     with pytest.raises(ops.QmoeUnsupported):
         ops.quantized_matmul(x, words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev), bits=8)
     w, s, b = synth.quant_weights(rng, (4, 128), 2048, bits=8)

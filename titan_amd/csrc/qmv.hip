@@ -386,7 +386,7 @@ namespace {
 #define QMV_AFTER(v)
 #endif
 
-template <int NV, int TL, int MODE, int RG, int GS, bool GATHER, bool XROWS>
+template <int NV, int TL, int MODE, int RG, int GS, bool GATHER, bool XROWS, int BITS = 4>
 __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   QMV_STAMP(ts_entry);
   // K = 2048 * NV + 512 * TL: NV whole chunks of 64 lanes x 32 elements and,
@@ -394,6 +394,9 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   // nothing and contribute zero: x = 0 there)
   constexpr int NC = NV + (TL > 0 ? 1 : 0);
   constexpr int KE = 2048 * NV + 512 * TL;
+  // 8-bit codes (plain rows, no tail): a lane's 32 codes are two adjacent 16-byte units
+  static_assert(BITS == 4 || (BITS == 8 && TL == 0 && MODE == 0), "8-bit: plain rows, K = 2048 * NV");
+  constexpr int WPC = BITS / 4;
   static_assert(KE % (8 * GS) == 0, "16-byte scale units per row");
   constexpr int OUTS = MODE == 1 ? RG : 2 * RG;
   constexpr int G = KE / GS;            // groups per row
@@ -422,7 +425,7 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
   e = min(max(e, 0), a.num_experts - 1);
   QMV_AFTER_S(e);
   QMV_STAMP(ts_id);
-  constexpr int64_t KW = KE / 8;
+  constexpr int64_t KW = KE * BITS / 32;
   const int64_t ebase = (int64_t)e * a.n_w;
   const int grp1 = MODE == 1 ? a.n_out + n0 : n0 + RG;
   // row of slot (group g, row i), clamped into the expert (slots past n_out are computed, not stored)
@@ -442,15 +445,17 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
       sbv[j] = *reinterpret_cast<const i32x4_t*>(base + row_of(seg & 1, rem / UPR) * G + (rem % UPR) * 8);
     }
   }
-  uint4 wv[2][RG][NC];
+  uint4 wv[2][RG][NC][WPC];
 #pragma unroll
   for (int g = 0; g < 2; ++g)
 #pragma unroll
     for (int i = 0; i < RG; ++i) {
-      const uint4* p = reinterpret_cast<const uint4*>(a.w + row_of(g, i) * KW) + lane;
+      const uint4* p = reinterpret_cast<const uint4*>(a.w + row_of(g, i) * KW) + WPC * lane;
 #pragma unroll
       for (int v = 0; v < NC; ++v)
-        wv[g][i][v] = (v < NV || tail_lane) ? load_nt(p + v * 64) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int c = 0; c < WPC; ++c)
+          wv[g][i][v][c] = (v < NV || tail_lane) ? load_nt(p + WPC * v * 64 + c) : make_uint4(0u, 0u, 0u, 0u);
     }
   XChunk xc[NC];
 #pragma unroll
@@ -459,10 +464,17 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint4 t = xa[v][q];
-      xc[v].p[4 * q + 0] = (t.x & 0xFFFFu) | (t.z << 16);
-      xc[v].p[4 * q + 1] = (t.x >> 16) | (t.z & 0xFFFF0000u);
-      xc[v].p[4 * q + 2] = (t.y & 0xFFFFu) | (t.w << 16);
-      xc[v].p[4 * q + 3] = (t.y >> 16) | (t.w & 0xFFFF0000u);
+      if constexpr (BITS == 8) {  // the pairing dot_chunk8 reads (load_x_chunk8)
+        xc[v].p[4 * q + 0] = (t.x & 0xFFFFu) | (t.y << 16);
+        xc[v].p[4 * q + 1] = (t.x >> 16) | (t.y & 0xFFFF0000u);
+        xc[v].p[4 * q + 2] = (t.z & 0xFFFFu) | (t.w << 16);
+        xc[v].p[4 * q + 3] = (t.z >> 16) | (t.w & 0xFFFF0000u);
+      } else {
+        xc[v].p[4 * q + 0] = (t.x & 0xFFFFu) | (t.z << 16);
+        xc[v].p[4 * q + 1] = (t.x >> 16) | (t.z & 0xFFFF0000u);
+        xc[v].p[4 * q + 2] = (t.y & 0xFFFFu) | (t.w << 16);
+        xc[v].p[4 * q + 3] = (t.y >> 16) | (t.w & 0xFFFF0000u);
+      }
       s += ((bf16lo(t.x) + bf16hi(t.x)) + (bf16lo(t.y) + bf16hi(t.y))) +
            ((bf16lo(t.z) + bf16hi(t.z)) + (bf16lo(t.w) + bf16hi(t.w)));
     }
@@ -492,7 +504,10 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
         const int gi = min((v * 2048 + lane * 32) / GS, G - 1);  // tail lanes past K: any group (x = 0)
         const float sv = bf16_to_f32(sbl[((0 * 2 + g) * RG + i) * G + gi]);
         const float bv = bf16_to_f32(sbl[((1 * 2 + g) * RG + i) * G + gi]);
-        acc += affine_chunk(dot_chunk(wv[g][i][v], xc[v], mv), xc[v].sum, sv, bv);
+        if constexpr (BITS == 8)
+          acc += affine_chunk8(dot_chunk8(wv[g][i][v][0], wv[g][i][v][WPC - 1], xc[v], mv), xc[v].sum, sv, bv);
+        else
+          acc += affine_chunk(dot_chunk(wv[g][i][v][0], xc[v], mv), xc[v].sum, sv, bv);
       }
       part[4 * g + i] = acc;
 #ifdef QMOE_QMV_STAMPS
@@ -1066,28 +1081,28 @@ bool pick_split(int64_t K, int* lpr, int* nv) {
   return false;
 }
 
-template <int MODE, int RG, int NV, int TL, int GS>
+template <int MODE, int RG, int NV, int TL, int GS, int BITS = 4>
 int launch_qmv64_k(const QmvArgs& a, dim3 grid, hipStream_t st) {
   if (MODE == 1) {
     qmv64_kernel<NV, TL, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
   } else if (!a.experts) {
-    qmv64_kernel<NV, TL, MODE, RG, GS, false, false><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, false, false, BITS><<<grid, dim3(64), 0, st>>>(a);
   } else if (a.x_rows) {
-    qmv64_kernel<NV, TL, MODE, RG, GS, true, true><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, true, true, BITS><<<grid, dim3(64), 0, st>>>(a);
   } else {
-    qmv64_kernel<NV, TL, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, true, false, BITS><<<grid, dim3(64), 0, st>>>(a);
   }
   return qmoe::launch_status("qmv64_kernel");
 }
 
 // K = 2048 * NV + 512 * TL; tails (TL > 0) are instantiated for group 64 only
-template <int MODE, int RG, int NV, int TL>
+template <int MODE, int RG, int NV, int TL, int BITS = 4>
 int launch_qmv64_tl(const QmvArgs& a, dim3 grid, hipStream_t st) {
   if constexpr (TL == 0) {
     switch (a.group_size) {
-      case 32: return launch_qmv64_k<MODE, RG, NV, 0, 32>(a, grid, st);
-      case 64: return launch_qmv64_k<MODE, RG, NV, 0, 64>(a, grid, st);
-      default: return launch_qmv64_k<MODE, RG, NV, 0, 128>(a, grid, st);
+      case 32: return launch_qmv64_k<MODE, RG, NV, 0, 32, BITS>(a, grid, st);
+      case 64: return launch_qmv64_k<MODE, RG, NV, 0, 64, BITS>(a, grid, st);
+      default: return launch_qmv64_k<MODE, RG, NV, 0, 128, BITS>(a, grid, st);
     }
   } else {
     return launch_qmv64_k<MODE, RG, NV, TL, 64>(a, grid, st);
@@ -1104,6 +1119,17 @@ int launch_qmv64_nv(const QmvArgs& a, dim3 grid, hipStream_t st) {
   }
 }
 
+// 8-bit codes: plain rows, K = 2048 * n
+template <int RG>
+int launch_qmv64_8(const QmvArgs& a, dim3 grid, hipStream_t st) {
+  switch (a.K / 2048) {
+    case 1: return launch_qmv64_tl<0, RG, 1, 0, 8>(a, grid, st);
+    case 2: return launch_qmv64_tl<0, RG, 2, 0, 8>(a, grid, st);
+    case 3: return launch_qmv64_tl<0, RG, 3, 0, 8>(a, grid, st);
+    default: return launch_qmv64_tl<0, RG, 4, 0, 8>(a, grid, st);
+  }
+}
+
 template <int MODE, int RG>
 int launch_qmv64(const QmvArgs& a, dim3 grid, hipStream_t st) {
   switch (a.K / 2048) {
@@ -1115,9 +1141,12 @@ int launch_qmv64(const QmvArgs& a, dim3 grid, hipStream_t st) {
 }
 
 // Shapes the 2048-chunk GEMV takes: K = 2048 * n + 512 * t (1 <= n <= 4,
-// t < 4, and t == 0 unless group_size == 64), 4-bit codes.
+// t < 4, and t == 0 unless group_size == 64) with 4-bit codes; K = 2048 * n
+// with 8-bit codes (plain rows only).
 bool qmv64_shape(int64_t K, int group_size, int bits) {
-  if (bits != 4 || K < 2048 || K % 512 || K / 2048 > 4) return false;
+  if (K < 2048 || K % 512 || K / 2048 > 4) return false;
+  if (bits == 8) return K % 2048 == 0;
+  if (bits != 4) return false;
   return K % 2048 == 0 || group_size == 64;
 }
 
@@ -1139,6 +1168,10 @@ int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st, int bits = 4) 
     b.blk_div = make_fastdiv((uint32_t)nblk);
     b.x_divf = make_fastdiv(a.x_rows ? 1u : (uint32_t)a.x_div);
     dim3 grid((unsigned)blocks), block(64);
+    if (bits == 8) {
+      if constexpr (MODE == 0) return launch_qmv64_8<RG>(b, grid, st);
+      return qmoe::fail(QMOE_ERR_UNSUPPORTED, "8-bit codes: plain rows only");
+    }
     return launch_qmv64<MODE, RG>(b, grid, st);
   }
   const int gpw = 64 / lpr;
@@ -1244,8 +1277,8 @@ int check_tiled(int64_t K, int64_t rows_per_expert, const void* x, const void* w
   return QMOE_OK;
 }
 
-// allow8: the entry point has 8-bit kernels (the plain row form); they need
-// a lane split (the qmv64 fast path is 4-bit only)
+// allow8: the entry point has 8-bit kernels (the plain row form): the qmv64
+// fast path at K = 2048 * n, a lane split otherwise
 int check_common(int64_t K, int group_size, int bits, int* lpr, int* nv, bool allow8 = false) {
   if (bits != 4 && !(allow8 && bits == 8))
     return qmoe::fail(QMOE_ERR_UNSUPPORTED, "bits=%d: this entry point has %s kernels", bits,
