@@ -66,9 +66,9 @@ def test_unsupported_configurations_say_so(L):
     dummy = ctypes.c_void_p(16)  # never dereferenced: rejected on the host
     rc = L.qmoe_gather_qmv(dummy, None, dummy, 4, 2048, dummy, dummy, dummy, 8, 128, 64, 3, dummy, None)
     assert rc == _lib.ERR_UNSUPPORTED and "bits=3" in _lib.last_error()
-    # 8-bit codes: no lane split past K = 4096, and no fused decode kernel
-    rc = L.qmoe_quantized_matmul(dummy, 1, 8192, dummy, dummy, dummy, 64, 64, 8, dummy, None)
-    assert rc == _lib.ERR_UNSUPPORTED and "K=8192" in _lib.last_error()
+    # 8-bit codes: K = 2048 * n (n <= 4) or a lane split (K <= 4096), and no fused decode kernel
+    rc = L.qmoe_quantized_matmul(dummy, 1, 10240, dummy, dummy, dummy, 64, 64, 8, dummy, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "K=10240" in _lib.last_error()
     rc = L.qmoe_moe_gate_up_swiglu(dummy, dummy, 1, 2, 2048, dummy, dummy, dummy, 4, 64, 64, 8, dummy, None)
     assert rc == _lib.ERR_UNSUPPORTED and "bits=8" in _lib.last_error()
     rc = L.qmoe_gather_qmv(dummy, None, dummy, 4, 2048, dummy, dummy, dummy, 8, 128, 48, 4, dummy, None)
