@@ -122,8 +122,8 @@ int qmoe_build_tiles(const int32_t* sorted_ids, int64_t n_rows,
  * Matrix-vector kernel: every row streams its expert's weights, so this is the
  * decode / small-batch path.  fp32 accumulation of the factored affine form
  * s*sum(x*q) + b*sum(x) (engine/patches/decode-fusion/fused_kernels.py:57-79),
- * bf16 output.  bits 4 or 8 (8-bit codes need K = 32*L*n with L in {4, 8, 16}
- * and n <= 8, so K <= 4096), group_size 32, 64 or 128
+ * bf16 output.  bits 4 or 8 (8-bit codes need K = 2048*n with n <= 4, or
+ * K = 32*L*n with L in {4, 8, 16} and n <= 8), group_size 32, 64 or 128
  * (engine/patches/smallm/kernel.py:38, 319-327). */
 int qmoe_gather_qmv(const uint16_t* x, const int32_t* x_rows,
                     const int32_t* experts, int64_t n_rows, int64_t K,
