@@ -677,7 +677,7 @@ def setup_cfg5(args, dev):
 
     return wl, [mk(i) for i in range(L)], {
         "bytes": per_call, "flops": synth.algorithmic_flops(5), "bound": "hbm",
-        "kernel": "qmv64_kernel<1, 0, 0, 2, 64, false, false, 8>", "sets": len(sets), "cycle_bytes": min(L, len(sets)) * per_call,
+        "kernel": "qmv64_kernel8<1, 2, 64, false, false>", "sets": len(sets), "cycle_bytes": min(L, len(sets)) * per_call,
         "workload": "dense quantized_matmul x [1,2048] . W [4096,2048] int8 codes g64"}
 
 

@@ -386,8 +386,8 @@ namespace {
 #define QMV_AFTER(v)
 #endif
 
-template <int NV, int TL, int MODE, int RG, int GS, bool GATHER, bool XROWS, int BITS = 4>
-__global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
+template <int NV, int TL, int MODE, int RG, int GS, bool GATHER, bool XROWS, int BITS>
+__device__ __forceinline__ void qmv64_rows(const QmvArgs& a) {
   QMV_STAMP(ts_entry);
   // K = 2048 * NV + 512 * TL: NV whole chunks of 64 lanes x 32 elements and,
   // when TL > 0, a tail chunk held by lanes < 16 * TL (the others load
@@ -544,6 +544,17 @@ __global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
     o[0] = ts_entry; o[1] = ts_args; o[2] = ts_id; o[3] = ts_first; o[4] = ts_reduced; o[5] = ts_stored;
   }
 #endif
+}
+
+// 4-bit codes; the 8-bit plain-row form is its own kernel name, so the 4-bit
+// kernels keep theirs in traces
+template <int NV, int TL, int MODE, int RG, int GS, bool GATHER, bool XROWS>
+__global__ __launch_bounds__(64) void qmv64_kernel(QmvArgs a) {
+  qmv64_rows<NV, TL, MODE, RG, GS, GATHER, XROWS, 4>(a);
+}
+template <int NV, int RG, int GS, bool GATHER, bool XROWS>
+__global__ __launch_bounds__(64) void qmv64_kernel8(QmvArgs a) {
+  qmv64_rows<NV, 0, 0, RG, GS, GATHER, XROWS, 8>(a);
 }
 
 // Block id -> work item, XCD-contiguous: the hardware deals consecutive block
@@ -1083,14 +1094,21 @@ bool pick_split(int64_t K, int* lpr, int* nv) {
 
 template <int MODE, int RG, int NV, int TL, int GS, int BITS = 4>
 int launch_qmv64_k(const QmvArgs& a, dim3 grid, hipStream_t st) {
+  if constexpr (BITS == 8) {
+    static_assert(MODE == 0 && TL == 0, "8-bit codes: plain rows, K = 2048 * NV");
+    if (!a.experts) qmv64_kernel8<NV, RG, GS, false, false><<<grid, dim3(64), 0, st>>>(a);
+    else if (a.x_rows) qmv64_kernel8<NV, RG, GS, true, true><<<grid, dim3(64), 0, st>>>(a);
+    else qmv64_kernel8<NV, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
+    return qmoe::launch_status("qmv64_kernel8");
+  }
   if (MODE == 1) {
     qmv64_kernel<NV, TL, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
   } else if (!a.experts) {
-    qmv64_kernel<NV, TL, MODE, RG, GS, false, false, BITS><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, false, false><<<grid, dim3(64), 0, st>>>(a);
   } else if (a.x_rows) {
-    qmv64_kernel<NV, TL, MODE, RG, GS, true, true, BITS><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, true, true><<<grid, dim3(64), 0, st>>>(a);
   } else {
-    qmv64_kernel<NV, TL, MODE, RG, GS, true, false, BITS><<<grid, dim3(64), 0, st>>>(a);
+    qmv64_kernel<NV, TL, MODE, RG, GS, true, false><<<grid, dim3(64), 0, st>>>(a);
   }
   return qmoe::launch_status("qmv64_kernel");
 }
