@@ -288,23 +288,36 @@ def timer(args):
 # ------------------------------------------------------------ measured peaks
 
 
+def peaks_lib():
+    """libqmoe_peaks.so (include/qmoe_peaks.h) through ctypes."""
+    import ctypes
+
+    from titan_amd import build as tbuild
+
+    L = ctypes.CDLL(str(tbuild.PEAKS_LIB))
+    c_int, c_vp = ctypes.c_int, ctypes.c_void_p
+    sigs = {"qmoe_peak_stream_read": [c_vp, ctypes.c_size_t, c_vp, c_vp],
+            "qmoe_peak_mfma_bf16": [c_int, c_vp, c_vp],
+            "qmoe_peak_mfma_i8": [c_int, c_vp, c_vp],
+            "qmoe_peak_launch": [c_int, c_vp],
+            "qmoe_peak_chain": [c_vp, c_int, c_int, c_vp, c_int, c_int, c_int, c_vp, c_vp]}
+    for name, argtypes in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = c_int
+        fn.argtypes = argtypes
+    return L
+
+
 def measure_peaks(dev, read_gib=4):
     """What this part sustains, with the probe kernels of libqmoe_peaks.so: a
     streaming read of `read_gib` GiB (beyond the 256 MB Infinity Cache) and
     dense bf16 / int8 MFMA loops over random register operands.  Medians of
     five timed runs after one warm-up."""
-    import ctypes
     import statistics
 
     import torch
-    from titan_amd import build as tbuild
 
-    L = ctypes.CDLL(str(tbuild.PEAKS_LIB))
-    for name in ("qmoe_peak_stream_read", "qmoe_peak_mfma_bf16", "qmoe_peak_mfma_i8"):
-        getattr(L, name).restype = ctypes.c_int
-    L.qmoe_peak_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
-    L.qmoe_peak_mfma_bf16.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    L.qmoe_peak_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    L = peaks_lib()
     nbytes = read_gib * 2 ** 30
     buf = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).random_()
     sink = torch.zeros(max(L.qmoe_peak_stream_blocks(), L.qmoe_peak_mfma_waves()), dtype=torch.int32, device=dev)
@@ -411,7 +424,32 @@ def setup_cfg1(args, dev):
                           torch.cuda.current_stream().cuda_stream)
         return f
 
+    # the per-call floor of this launch shape (libqmoe_peaks.so): the same
+    # 1280 single-wave blocks doing nothing, and walking the dependent chain
+    # (arguments -> expert id -> the first 1 KiB weight row) over the same
+    # ids and weight sets
+    P = peaks_lib()
+    sink = torch.zeros(1280, dtype=torch.int32, device=dev)
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(f"floor probe failed (code {rc})")
+
+    def mk_chain(i):
+        w = sets[i % len(sets)][0]
+        idx = idxs[i]
+
+        def f():
+            check(P.qmoe_peak_chain(idx.data_ptr(), 10, E, w.data_ptr(), 1024, 1024, 8, sink.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream))
+        return f
+
+    def launch():
+        check(P.qmoe_peak_launch(1280, torch.cuda.current_stream().cuda_stream))
+
     return wl, [mk_mlx(i) for i in range(L)], {
+        "floor": {"launch": [launch] * L, "chain": [mk_chain(i) for i in range(L)],
+                  "chain_bytes": 1280 * 1024 + 10 * 4},
         "bytes": per_call, "flops": synth.algorithmic_flops(1), "bound": "hbm",
         "kernel": "qmv64_kernel<1, 0, 1, 4, 64, true, false>", "sets": len(sets),
         "cycle_bytes": L * per_call,
@@ -1056,6 +1094,13 @@ def main():
             sec_alt, _ta = timer(args)(alt, steps, args.warmup, dev)
             res[label] = round(sec_alt * 1e6, 3)
             del alt, _ta
+        if "floor" in meta:
+            fl = meta.pop("floor")
+            sec_l, _tl = timer(args)(fl["launch"], steps, args.warmup, dev)
+            sec_c, _tc = timer(args)(fl["chain"], steps, args.warmup, dev)
+            res["floor"] = {"launch_us": round(sec_l * 1e6, 3), "chain_us": round(sec_c * 1e6, 3),
+                            "chain_bytes": fl["chain_bytes"]}
+            del fl, _tl, _tc
         for label, ex, ex_flops in meta.get("extras", ()):
             sec_ex, _te = timer(args)(ex, steps, args.warmup, dev)
             res[label] = {"us_per_call": round(sec_ex * 1e6, 3), "TOP/s": round(ex_flops / sec_ex / 1e12, 1),
@@ -1095,6 +1140,18 @@ def main():
     if peaks:
         roof["peak_measured"] = peaks["hbm_read_GBps"]
         roof["frac_measured"] = round(gbs / peaks["hbm_read_GBps"], 4)
+    fl = results.get(1, {}).get("floor")
+    if fl is not None:
+        # per-call floor of one launch that must learn its experts before
+        # asking for their weights: the chain probe (launch, arguments, expert
+        # id, first row, store) plus the remaining bytes at the measured read rate
+        floor = dict(fl)
+        if peaks:
+            stream_us = (meta["bytes"] - fl["chain_bytes"]) / (peaks["hbm_read_GBps"] * 1e3)
+            floor["stream_rest_us"] = round(stream_us, 3)
+            floor["model_us"] = round(fl["chain_us"] + stream_us, 3)
+            floor["frac_of_model"] = round((fl["chain_us"] + stream_us) / (sec * 1e6), 4)
+        roof["floor"] = floor
     line = {
         "metric": METRIC,
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

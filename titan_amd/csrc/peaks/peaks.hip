@@ -105,6 +105,30 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_i8_kernel(int iters, uint32
   if (threadIdx.x % 64 == 0) sink[gid / 64] = (uint32_t)s;
 }
 
+// Per-call floor of a one-launch decode step, in two parts.  The launch
+// alone: single-wave blocks that do nothing.  The dependent chain: each
+// single-wave block reads its kernel arguments, then the expert id of its
+// slot, then one 16-byte unit per lane of the first weight row of its row
+// block (one row of 64 units, as the decode kernel's first row), and stores
+// one word -- the three memory round trips a decode wave cannot overlap.
+__global__ __launch_bounds__(64) void launch_probe_kernel() {}
+
+__global__ __launch_bounds__(64) void chain_probe_kernel(const int32_t* __restrict__ ids, int blocks_per_slot,
+                                                         int num_experts, const i32x4_t* __restrict__ w,
+                                                         int64_t expert_units, int64_t block_units,
+                                                         uint32_t* __restrict__ sink) {
+  const uint32_t b = blockIdx.x;
+  const uint32_t slot = b / (uint32_t)blocks_per_slot;
+  const uint32_t rb = b - slot * (uint32_t)blocks_per_slot;
+  int e = ids[slot];
+  e = min(max(e, 0), num_experts - 1);
+  const i32x4_t v = __builtin_nontemporal_load(w + (int64_t)e * expert_units + (int64_t)rb * block_units +
+                                               threadIdx.x);
+  uint32_t acc = (uint32_t)(v[0] ^ v[1] ^ v[2] ^ v[3]);
+  for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m, 64);
+  if (threadIdx.x == 0) sink[b] = acc;
+}
+
 int status() { return hipGetLastError() == hipSuccess ? 0 : 3; }
 
 }  // namespace
@@ -123,6 +147,30 @@ extern "C" int qmoe_peak_mfma_waves(void) { return kMfmaBlocks * kMfmaThreads / 
 extern "C" int qmoe_peak_mfma_bf16(int iters, uint32_t* sink, void* stream) {
   if (iters <= 0 || !sink) return 1;
   mfma_bf16_kernel<<<dim3(kMfmaBlocks), dim3(kMfmaThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(iters, sink);
+  return status();
+}
+
+extern "C" int qmoe_peak_launch(int blocks, void* stream) {
+  if (blocks <= 0) return 1;
+  launch_probe_kernel<<<dim3(blocks), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>();
+  return status();
+}
+
+extern "C" int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, const void* w, int rows_per_expert,
+                               int row_bytes, int rows_per_block, uint32_t* sink, void* stream) {
+  // every block reads units [0, 64) of row rb * rows_per_block of its expert:
+  // in bounds when a row holds at least 64 units and the row blocks tile the rows
+  if (!ids || !w || !sink || slots <= 0 || num_experts <= 0 || rows_per_expert <= 0 || rows_per_block <= 0 ||
+      row_bytes % 16 || row_bytes / 16 < 64 || rows_per_expert % rows_per_block ||
+      (reinterpret_cast<uintptr_t>(w) & 15))
+    return 1;
+  const int blocks_per_slot = rows_per_expert / rows_per_block;
+  const int64_t row_units = row_bytes / 16;
+  chain_probe_kernel<<<dim3((uint32_t)slots * (uint32_t)blocks_per_slot), dim3(64), 0,
+                       reinterpret_cast<hipStream_t>(stream)>>>(ids, blocks_per_slot, num_experts,
+                                                                static_cast<const i32x4_t*>(w),
+                                                                (int64_t)rows_per_expert * row_units,
+                                                                (int64_t)rows_per_block * row_units, sink);
   return status();
 }
 

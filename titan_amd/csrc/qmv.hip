@@ -557,6 +557,155 @@ __global__ __launch_bounds__(64) void qmv64_kernel8(QmvArgs a) {
   qmv64_rows<NV, 0, 0, RG, GS, GATHER, XROWS, 8>(a);
 }
 
+// Two per-lane partials -> 64-lane sums by reduce8's tree (the same lane
+// pairings at every level, so a slot summed here is bit-identical to the same
+// slot summed there): lanes < 32 hold the sum of a, lanes >= 32 that of b.
+__device__ __forceinline__ float reduce2(float a, float b, int lane) {
+  float r = fold32(a, b);
+  r = fold16(r, r);
+  return sum8(fold8(r, r, lane));
+}
+
+// Fused gate_up + SwiGLU for one token (every pair reads x row 0), flat form:
+// wave b takes the kFlatRG consecutive slots f = b*kFlatRG .. of the
+// n_pairs * n_out list (pair f / n_out, index f % n_out), so a wave may span
+// two pairs, i.e. two experts (kFlatRG <= n_out).  Ten experts x 512 indices
+// are then 1024 waves, one per SIMD of a 256-CU part, where the four-index
+// waves of qmv64_kernel number 1280 and put two waves -- 16 rows of
+// arithmetic -- on a quarter of the SIMDs, which finish last.  Per lane and row
+// the arithmetic is qmv64_kernel's (same loads, same chunk sums), and the fifth
+// slot's reduction follows reduce8's tree, so every output is bit-identical to
+// that kernel's.  Slots past the list repeat its last entry and are not stored.
+constexpr int kFlatRG = 5;
+
+template <int NV, int GS>
+__global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
+  constexpr int KE = 2048 * NV;
+  constexpr int G = KE / GS;            // groups per row
+  constexpr int UPR = G / 8;            // 16-byte scale units per row
+  constexpr int UNITS = 4 * kFlatRG * UPR;  // [slot][gate/up][scale/bias][UPR]
+  constexpr int UPL = (UNITS + 63) / 64;
+  constexpr int64_t KW = KE / 8;
+  __shared__ __attribute__((aligned(16))) uint16_t sbl[UNITS * 8];
+  const int lane = threadIdx.x;
+  // every kernel argument the wave reads, in one batch of scalar loads (left
+  // alone, the compiler spreads them over three dependent round trips)
+  const uint16_t* ax = a.x;
+  const int32_t* aexp = a.experts;
+  const uint32_t* aw = a.w;
+  const uint16_t* as_ = a.s;
+  const uint16_t* ab = a.b;
+  uint16_t* aout = a.out;
+  const int nexp = a.num_experts, n_out = a.n_out, n_w = a.n_w;
+  const uint32_t npairs = (uint32_t)a.n_pairs, bd_m = a.blk_div.m, bd_s = a.blk_div.s;
+  asm volatile("" ::"s"(ax), "s"(aexp), "s"(aw), "s"(as_), "s"(ab), "s"(aout), "s"(nexp), "s"(n_out), "s"(n_w),
+               "s"(npairs), "s"(bd_m), "s"(bd_s));
+  const FastDiv bd{(uint32_t)n_out, bd_m, bd_s};  // n_out
+  const uint32_t total = npairs * (uint32_t)n_out;  // < 2^31 (host)
+  const uint32_t f0 = blockIdx.x * (uint32_t)kFlatRG;
+  const uint32_t flast = min(f0 + (uint32_t)(kFlatRG - 1), total - 1);
+  const uint32_t ra = fast_div(f0, bd);
+  const uint32_t rb = fast_div(flast, bd);
+  uint4 xa[NV][4];
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xa[v][q] = reinterpret_cast<const uint4*>(ax + v * 2048 + lane * 32)[q];
+  // the two expert ids as scalar loads while x is in flight (written as plain
+  // loads after the batch above they would go through the vector path)
+  int ea, eb;
+  asm volatile(
+      "s_load_dword %0, %2, 0x0\n\t"
+      "s_load_dword %1, %3, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(ea), "=&s"(eb)
+      : "s"(aexp + ra), "s"(aexp + rb)
+      : "memory");
+  ea = min(max(ea, 0), nexp - 1);
+  eb = min(max(eb, 0), nexp - 1);
+  const uint32_t fb = (ra + 1) * (uint32_t)n_out;  // first slot of the second pair
+  // weight row of slot s (0..kFlatRG-1), gate (g = 0) or up (g = 1), as a row
+  // index of the whole weight tensor (< 2^31: host)
+  auto slot_row = [&](uint32_t s, uint32_t g) -> uint32_t {
+    const uint32_t f = min(f0 + s, total - 1);
+    const bool second = f >= fb;
+    const uint32_t i = f - (second ? fb : fb - (uint32_t)n_out);
+    return (uint32_t)(second ? eb : ea) * (uint32_t)n_w + (g ? (uint32_t)n_out : 0u) + i;
+  };
+
+  i32x4_t sbv[UPL];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = lane + 64 * j;
+    if (UNITS % 64 == 0 || u < UNITS) {
+      const uint32_t seg = (uint32_t)u / UPR, up = (uint32_t)u % UPR;  // seg = (s * 2 + g) * 2 + arr
+      const uint16_t* base = (seg & 1) ? ab : as_;
+      sbv[j] = *reinterpret_cast<const i32x4_t*>(base + (uint64_t)slot_row(seg >> 2, (seg >> 1) & 1) * G + up * 8);
+    }
+  }
+  uint4 wv[2][kFlatRG][NV];
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int s = 0; s < kFlatRG; ++s) {
+      const uint4* p = reinterpret_cast<const uint4*>(aw + (uint64_t)slot_row((uint32_t)s, (uint32_t)g) * KW) + lane;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) wv[g][s][v] = load_nt(p + v * 64);
+    }
+  XChunk xc[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 t = xa[v][q];
+      xc[v].p[4 * q + 0] = (t.x & 0xFFFFu) | (t.z << 16);
+      xc[v].p[4 * q + 1] = (t.x >> 16) | (t.z & 0xFFFF0000u);
+      xc[v].p[4 * q + 2] = (t.y & 0xFFFFu) | (t.w << 16);
+      xc[v].p[4 * q + 3] = (t.y >> 16) | (t.w & 0xFFFF0000u);
+      sum += ((bf16lo(t.x) + bf16hi(t.x)) + (bf16lo(t.y) + bf16hi(t.y))) +
+             ((bf16lo(t.z) + bf16hi(t.z)) + (bf16lo(t.w) + bf16hi(t.w)));
+    }
+    xc[v].sum = sum;
+  }
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = lane + 64 * j;
+    if (UNITS % 64 == 0 || u < UNITS) *reinterpret_cast<i32x4_t*>(sbl + u * 8) = sbv[j];
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the staged words are visible to the wave
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t mv = magic_vgpr();
+  // slots 0..3 as reduce8's eight partials (gate q, then up q at 4 + q), slot 4 apart
+  float part[8], last[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int s = 0; s < kFlatRG; ++s) {
+      float acc = 0.f;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int gi = (v * 2048 + lane * 32) / GS;
+        const float sv = bf16_to_f32(sbl[((s * 2 + g) * 2 + 0) * G + gi]);
+        const float bv = bf16_to_f32(sbl[((s * 2 + g) * 2 + 1) * G + gi]);
+        acc += affine_chunk(dot_chunk(wv[g][s][v], xc[v], mv), xc[v].sum, sv, bv);
+      }
+      if (s < 4) part[4 * g + s] = acc;
+      else last[g] = acc;
+    }
+  const float t = reduce8(part, lane);         // lanes 8q: gate q, lanes 8q + 32: up q (q < 4)
+  const float t4 = reduce2(last[0], last[1], lane);  // lanes < 32: gate 4, lanes >= 32: up 4
+  auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
+  auto sw4 = __builtin_amdgcn_permlane32_swap(as_u(t4), as_u(t4), false, false);
+  // lane 8q stores slot q (q < 4), lane 1 slot 4
+  const int q = lane >> 3;
+  const bool st4 = lane == 1;
+  const float gate = st4 ? t4 : t, up = as_f(st4 ? sw4[1] : sw[1]);
+  const uint32_t f = f0 + (st4 ? 4u : (uint32_t)q);
+  if (lane < 32 && ((lane & 7) == 0 || st4) && f < total)
+    aout[f] = (uint16_t)f32_to_bf16(gate / (1.0f + expf(-gate)) * up);
+}
+
 // Block id -> work item, XCD-contiguous: the hardware deals consecutive block
 // ids round-robin to the 8 XCDs, so with nb % 8 == 0 item v = (b % 8) * nb/8
 // + b / 8 puts consecutive items -- row groups that share 128-byte code lines
@@ -1168,12 +1317,57 @@ bool qmv64_shape(int64_t K, int group_size, int bits) {
   return K % 2048 == 0 || group_size == 64;
 }
 
+// SIMDs of the current device (four per CU), looked up once.
+int simd_count() {
+  static int simds = 0;
+  if (!simds) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      simds = 4 * n;
+    if (simds <= 0) simds = 1024;
+  }
+  return simds;
+}
+
+// One token's fused gate_up on qmv64_flat_kernel when that lowers the rows of
+// arithmetic on the busiest SIMD: waves of RG indices compute 2 * RG rows, and
+// ceil(waves / SIMDs) of them share a SIMD.  Returns -1 when the flat form does
+// not apply or is no better.
+int launch_qmv_flat(const QmvArgs& a, hipStream_t st) {
+  if (a.x_rows || a.n_pairs != a.x_div || a.n_out < kFlatRG || a.K % 2048) return -1;
+  const int64_t total = a.n_pairs * (int64_t)a.n_out;
+  if (total <= 0 || total > 0x7FFFFFFF || (int64_t)a.num_experts * a.n_w > 0x7FFFFFFF) return -1;
+  const int64_t S = simd_count();
+  const int64_t waves4 = a.n_pairs * ((a.n_out + QMOE_QMV_RG_GU - 1) / QMOE_QMV_RG_GU);
+  const int64_t waves5 = (total + kFlatRG - 1) / kFlatRG;
+  if ((waves5 + S - 1) / S * (2 * kFlatRG) >= (waves4 + S - 1) / S * (2 * QMOE_QMV_RG_GU)) return -1;
+  QmvArgs b = a;
+  b.blk_div = make_fastdiv((uint32_t)a.n_out);
+  dim3 grid((unsigned)waves5), block(64);
+#define QMV_FLAT(NV_, GS_) \
+  if (a.K == 2048 * NV_ && a.group_size == GS_) { \
+    qmv64_flat_kernel<NV_, GS_><<<grid, block, 0, st>>>(b); \
+    return qmoe::launch_status("qmv64_flat_kernel"); \
+  }
+#define QMV_FLAT_GS(NV_) QMV_FLAT(NV_, 32) QMV_FLAT(NV_, 64) QMV_FLAT(NV_, 128)
+  QMV_FLAT_GS(1) QMV_FLAT_GS(2) QMV_FLAT_GS(3) QMV_FLAT_GS(4)
+#undef QMV_FLAT_GS
+#undef QMV_FLAT
+  return -1;
+}
+
 template <int MODE>
 int launch_qmv(const QmvArgs& a, int lpr, int nv, hipStream_t st, int bits = 4) {
   // qmv64 reads scales and biases 16 bytes at a time: G % 8 == 0 and aligned arrays
   const bool sb_ok = (a.K / a.group_size) % 8 == 0 && qmoe::aligned16(a.s) && qmoe::aligned16(a.b);
   if (qmv64_shape(a.K, a.group_size, bits) && (sb_ok || lpr == 0)) {
     if (!sb_ok) return qmoe::fail(QMOE_ERR_UNSUPPORTED, "scales and biases must be 16-byte aligned");
+    if constexpr (MODE == 1) {
+      if (bits == 4) {
+        const int rc = launch_qmv_flat(a, st);
+        if (rc >= 0) return rc;
+      }
+    }
     constexpr int RG = MODE == 1 ? QMOE_QMV_RG_GU : QMOE_QMV_RG_DENSE;
     constexpr int outs = MODE == 1 ? RG : 2 * RG;
     const int64_t nblk = (a.n_out + outs - 1) / outs;
