@@ -144,7 +144,7 @@ def calibration_copy(dev, mib=CALIBRATION_MIB, reps=5):
 # `--traffic` measures them live (rocprofv3 children started before this
 # process touches the GPU); otherwise the committed summary supplies them.
 
-TRAFFIC_KERNEL = "qmv64_kernel<1, 0, 1, 4, 64, true, false>"  # the decode gate_up + SwiGLU kernel (bench workload 1)
+TRAFFIC_KERNEL = "qmv64_flat_kernel<1, 64>"  # the one-token decode gate_up + SwiGLU kernel (bench workload 1)
 TRAFFIC_PROFILE = ROOT / "profiles" / "qmv64_decode_gate_up.traffic.txt"
 
 
@@ -451,7 +451,7 @@ def setup_cfg1(args, dev):
         "floor": {"launch": [launch] * L, "chain": [mk_chain(i) for i in range(L)],
                   "chain_bytes": 1280 * 1024 + 10 * 4},
         "bytes": per_call, "flops": synth.algorithmic_flops(1), "bound": "hbm",
-        "kernel": "qmv64_kernel<1, 0, 1, 4, 64, true, false>", "sets": len(sets),
+        "kernel": "qmv64_flat_kernel<1, 64>", "sets": len(sets),
         "cycle_bytes": L * per_call,
         "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(L)]),
         "workload": "decode gate_up gather_qmm + SwiGLU: 1 token, H=2048, E=256, top_k=10, "
@@ -791,7 +791,7 @@ def run_widths(args, dev):
         del routes, lhs, idx
     return {"workload": "decode widths: T tokens x top-10 of E=256, gate_up + SwiGLU, W [256,1024,2048] int4 g64; "
                         "decode GEMV vs route + SwiGLU grouped GEMM",
-            "kernel": "qmv64_kernel<1, 0, 1, 4, 64, true, false> | route_* + gemm_bf16_kernel<true, true>",
+            "kernel": "qmv64_flat_kernel<1, 64> (T = 1), qmv64_kernel<1, 0, 1, 4, 64, true, false> (T > 1) | route_* + gemm_bf16_kernel<true, true>",
             "widths": res}
 
 

@@ -557,6 +557,15 @@ __global__ __launch_bounds__(64) void qmv64_kernel8(QmvArgs a) {
   qmv64_rows<NV, 0, 0, RG, GS, GATHER, XROWS, 8>(a);
 }
 
+// Block id -> work item, XCD-contiguous: the hardware deals consecutive block
+// ids round-robin to the 8 XCDs, so with nb % 8 == 0 item v = (b % 8) * nb/8
+// + b / 8 puts consecutive items -- row groups that share 128-byte code lines
+// or a 256-byte scale|bias chunk of the tile layout -- on one XCD, where the
+// second reader finds the line in that XCD's L2.  A permutation of [0, nb).
+__device__ __forceinline__ uint32_t xcd_item(uint32_t b, uint32_t nb) {
+  return (nb & 7u) ? b : (b & 7u) * (nb >> 3) + (b >> 3);
+}
+
 // Two per-lane partials -> 64-lane sums by reduce8's tree (the same lane
 // pairings at every level, so a slot summed here is bit-identical to the same
 // slot summed there): lanes < 32 hold the sum of a, lanes >= 32 that of b.
@@ -602,7 +611,10 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
                "s"(npairs), "s"(bd_m), "s"(bd_s));
   const FastDiv bd{(uint32_t)n_out, bd_m, bd_s};  // n_out
   const uint32_t total = npairs * (uint32_t)n_out;  // < 2^31 (host)
-  const uint32_t f0 = blockIdx.x * (uint32_t)kFlatRG;
+  // consecutive waves on one XCD (xcd_item): the scale and bias lines that
+  // two neighbouring waves split (five rows of 64 bytes each) are then fetched
+  // into one L2, once
+  const uint32_t f0 = xcd_item(blockIdx.x, gridDim.x) * (uint32_t)kFlatRG;
   const uint32_t flast = min(f0 + (uint32_t)(kFlatRG - 1), total - 1);
   const uint32_t ra = fast_div(f0, bd);
   const uint32_t rb = fast_div(flast, bd);
@@ -623,14 +635,19 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
       : "memory");
   ea = min(max(ea, 0), nexp - 1);
   eb = min(max(eb, 0), nexp - 1);
-  const uint32_t fb = (ra + 1) * (uint32_t)n_out;  // first slot of the second pair
-  // weight row of slot s (0..kFlatRG-1), gate (g = 0) or up (g = 1), as a row
-  // index of the whole weight tensor (< 2^31: host)
+  // Slot s (0..kFlatRG-1) is list entry min(f0 + s, total - 1): in pair ra
+  // below sp, in pair ra + 1 (= rb) from sp on.  Its gate (g = 0) or up (g = 1)
+  // weight row, as a row index of the whole weight tensor (< 2^31: host), is
+  // row_a + s or row_b + s (+ n_out for up); row_b may wrap below zero, and
+  // adding s >= sp brings it back (exact modulo 2^32).
+  const uint32_t fb = (ra + 1) * (uint32_t)n_out;  // list entry of the second pair's index 0
+  const uint32_t sp = fb - f0;                     // >= 1
+  const uint32_t smax = total - 1 - f0;
+  const uint32_t row_a = (uint32_t)ea * (uint32_t)n_w + f0 - (fb - (uint32_t)n_out);
+  const uint32_t row_b = (uint32_t)eb * (uint32_t)n_w + f0 - fb;
   auto slot_row = [&](uint32_t s, uint32_t g) -> uint32_t {
-    const uint32_t f = min(f0 + s, total - 1);
-    const bool second = f >= fb;
-    const uint32_t i = f - (second ? fb : fb - (uint32_t)n_out);
-    return (uint32_t)(second ? eb : ea) * (uint32_t)n_w + (g ? (uint32_t)n_out : 0u) + i;
+    const uint32_t se = min(s, smax);
+    return (se < sp ? row_a : row_b) + se + (g ? (uint32_t)n_out : 0u);
   };
 
   i32x4_t sbv[UPL];
@@ -704,15 +721,6 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
   const uint32_t f = f0 + (st4 ? 4u : (uint32_t)q);
   if (lane < 32 && ((lane & 7) == 0 || st4) && f < total)
     aout[f] = (uint16_t)f32_to_bf16(gate / (1.0f + expf(-gate)) * up);
-}
-
-// Block id -> work item, XCD-contiguous: the hardware deals consecutive block
-// ids round-robin to the 8 XCDs, so with nb % 8 == 0 item v = (b % 8) * nb/8
-// + b / 8 puts consecutive items -- row groups that share 128-byte code lines
-// or a 256-byte scale|bias chunk of the tile layout -- on one XCD, where the
-// second reader finds the line in that XCD's L2.  A permutation of [0, nb).
-__device__ __forceinline__ uint32_t xcd_item(uint32_t b, uint32_t nb) {
-  return (nb & 7u) ? b : (b & 7u) * (nb >> 3) + (b >> 3);
 }
 
 // qmv64 over tile-layout weights (group 64), plain row form: the code chunk of
