@@ -792,7 +792,8 @@ def test_fused_decode_group_sizes(dev, orc, gs):
 
 
 @pytest.mark.parametrize("k,K,gs", [(10, 2048, 64), (9, 2048, 64), (10, 2048, 32), (9, 2048, 128),
-                                    (10, 4096, 64), (9, 8192, 64)])
+                                    (10, 4096, 64), (10, 6144, 128), (9, 6144, 32), (9, 8192, 64),
+                                    (10, 8192, 128)])
 def test_gate_up_one_token_flat_waves(dev, orc, k, K, gs):
     """One token's fused gate_up + SwiGLU runs on waves of five consecutive
     (pair, index) slots (qmv64_flat_kernel: ten experts x 512 indices make 1024
@@ -801,7 +802,7 @@ def test_gate_up_one_token_flat_waves(dev, orc, k, K, gs):
     match bit for bit, and both stay within the bar of the oracle."""
     say(f"gate_up one token flat waves k={k} K={K} gs={gs}")
     rng = np.random.default_rng(1000 + k + K + gs)
-    E, I = 256, 512
+    E, I = (256 if K <= 4096 else 32), 512
     w, s, b = synth.quant_weights(rng, (E, 2 * I), K, group_size=gs)
     x = synth.bf16_bits(rng.normal(size=(1, K)).astype(np.float32))
     idx = rng.choice(E, k, replace=False).astype(np.int32)[None]
