@@ -858,8 +858,8 @@ SETUPS = {0: setup_cfg0, 1: setup_cfg1, 2: setup_cfg2, 3: setup_cfg3, 4: setup_c
 
 
 def decode_phases(args, dev, samples=16):
-    """Workload 1 through the measurement build libqmoe_stamps.so, whose decode
-    GEMV writes s_memrealtime stamps (10 ns ticks) per block: entry, kernel
+    """Workload 1 through the measurement build libqmoe_stamps.so, whose one-token
+    decode GEMV writes s_memrealtime stamps (10 ns ticks) per block: entry, kernel
     arguments ready, expert id ready, first weight row consumed, all rows
     consumed and reduced, output store acknowledged.  The cycle is replayed
     as time_graph does; after each of `samples` window replays the stamps of
@@ -897,7 +897,7 @@ def decode_phases(args, dev, samples=16):
     stamped = [mk(i) for i in range(len(cycle))]
     sec, tinfo = time_graph(stamped, args.steps, args.warmup, dev)
     sec_prod, _ = time_graph(cycle, args.steps, args.warmup, dev)
-    nb = 1280  # blocks of one launch: 10 experts x 512 gate/up row pairs / 4
+    nb = 1024  # blocks of one launch: 10 experts x 512 gate/up row pairs / 5 (the flat one-token kernel)
     names = ["entry", "args", "id", "first_row", "reduced", "stored"]
     buf = np.zeros(nb * len(names), np.uint64)
     rows = []
@@ -929,8 +929,7 @@ def decode_phases(args, dev, samples=16):
         "product_us_per_call": round(sec_prod * 1e6, 3),
         "samples": samples,
         "workload": meta["workload"],
-        "note": "stamps in 10 ns ticks; the stamped build loads the expert id through the vector path "
-                "(the timer intrinsic keeps the compiler from proving the id load scalar-safe)",
+        "note": "stamps in 10 ns ticks, lane 0 of each of the flat kernel's 1024 single-wave blocks",
     }
     return res
 

@@ -596,6 +596,7 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
   constexpr int UPL = (UNITS + 63) / 64;
   constexpr int64_t KW = KE / 8;
   __shared__ __attribute__((aligned(16))) uint16_t sbl[UNITS * 8];
+  QMV_STAMP(ts_entry);
   const int lane = threadIdx.x;
   // every kernel argument the wave reads, in one batch of scalar loads (left
   // alone, the compiler spreads them over three dependent round trips)
@@ -609,12 +610,14 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
   const uint32_t npairs = (uint32_t)a.n_pairs, bd_m = a.blk_div.m, bd_s = a.blk_div.s;
   asm volatile("" ::"s"(ax), "s"(aexp), "s"(aw), "s"(as_), "s"(ab), "s"(aout), "s"(nexp), "s"(n_out), "s"(n_w),
                "s"(npairs), "s"(bd_m), "s"(bd_s));
+  QMV_STAMP(ts_args);
   const FastDiv bd{(uint32_t)n_out, bd_m, bd_s};  // n_out
   const uint32_t total = npairs * (uint32_t)n_out;  // < 2^31 (host)
   // consecutive waves on one XCD (xcd_item): the scale and bias lines that
   // two neighbouring waves split (five rows of 64 bytes each) are then fetched
   // into one L2, once
-  const uint32_t f0 = xcd_item(blockIdx.x, gridDim.x) * (uint32_t)kFlatRG;
+  // (the grid size from the batch above: gridDim.x would cost another dependent load)
+  const uint32_t f0 = xcd_item(blockIdx.x, (total + kFlatRG - 1) / kFlatRG) * (uint32_t)kFlatRG;
   const uint32_t flast = min(f0 + (uint32_t)(kFlatRG - 1), total - 1);
   const uint32_t ra = fast_div(f0, bd);
   const uint32_t rb = fast_div(flast, bd);
@@ -633,6 +636,9 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
       : "=&s"(ea), "=&s"(eb)
       : "s"(aexp + ra), "s"(aexp + rb)
       : "memory");
+  QMV_AFTER_S(ea);
+  QMV_AFTER_S(eb);
+  QMV_STAMP(ts_id);
   ea = min(max(ea, 0), nexp - 1);
   eb = min(max(eb, 0), nexp - 1);
   // Slot s (0..kFlatRG-1) is list entry min(f0 + s, total - 1): in pair ra
@@ -695,6 +701,9 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
   const uint32_t mv = magic_vgpr();
   // slots 0..3 as reduce8's eight partials (gate q, then up q at 4 + q), slot 4 apart
   float part[8], last[2];
+#ifdef QMOE_QMV_STAMPS
+  uint64_t ts_first = 0;
+#endif
 #pragma unroll
   for (int g = 0; g < 2; ++g)
 #pragma unroll
@@ -709,9 +718,19 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
       }
       if (s < 4) part[4 * g + s] = acc;
       else last[g] = acc;
+#ifdef QMOE_QMV_STAMPS
+      if (g == 0 && s == 0) {
+        QMV_AFTER(acc);
+        QMV_STAMP(ts_first_);
+        ts_first = ts_first_;
+      }
+#endif
     }
   const float t = reduce8(part, lane);         // lanes 8q: gate q, lanes 8q + 32: up q (q < 4)
   const float t4 = reduce2(last[0], last[1], lane);  // lanes < 32: gate 4, lanes >= 32: up 4
+  QMV_AFTER(t);
+  QMV_AFTER(t4);
+  QMV_STAMP(ts_reduced);
   auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
   auto sw4 = __builtin_amdgcn_permlane32_swap(as_u(t4), as_u(t4), false, false);
   // lane 8q stores slot q (q < 4), lane 1 slot 4
@@ -721,6 +740,14 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
   const uint32_t f = f0 + (st4 ? 4u : (uint32_t)q);
   if (lane < 32 && ((lane & 7) == 0 || st4) && f < total)
     aout[f] = (uint16_t)f32_to_bf16(gate / (1.0f + expf(-gate)) * up);
+#ifdef QMOE_QMV_STAMPS
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  QMV_STAMP(ts_stored);
+  if (lane == 0 && blockIdx.x < kStampBlocks) {
+    uint64_t* o = qmv_stamps + (size_t)blockIdx.x * kStampsPerBlock;
+    o[0] = ts_entry; o[1] = ts_args; o[2] = ts_id; o[3] = ts_first; o[4] = ts_reduced; o[5] = ts_stored;
+  }
+#endif
 }
 
 // qmv64 over tile-layout weights (group 64), plain row form: the code chunk of
