@@ -27,18 +27,26 @@
 //     each lane ends up owning four consecutive output columns per register
 //     quad and the epilogue stores 8 bytes at a time.
 //
+// The k-steps are software-pipelined inside each wave: while the MFMAs of
+// k-step s issue, one per slot, the wave reads the activation fragments of
+// k-step s + 1 and dequantises its weight fragment between them, so the
+// matrix core's busy cycles cover the wave's own vector work.
+//
 // Data movement: every operand byte reaches LDS through asynchronous copies
 // (global_load_lds_dwordx4 / _dword from inline assembly, so the copies stay
-// in flight across iterations with explicit wait counts) into a ring of
-// kStages stages.  A stage holds
+// in flight across iterations with explicit wait counts; the weight side
+// from wave-uniform SGPR bases) into a ring of stages.  A stage holds
 //   A  the tile's activation rows for the group, gathered through x_rows,
-//      128 x 128 bytes, 16-byte units XOR-swizzled by row (swz) so operand
-//      reads are bank-conflict free; only the subtiles the tile has are copied;
+//      32 x 128 bytes per row subtile, 16-byte units XOR-swizzled by row (swz)
+//      so operand reads are bank-conflict free; only the subtiles the tile
+//      has are copied;
 //   B  each wave's 64 columns of packed codes (16 bytes per lane and subtile);
 //   S  the 64 columns' scales and biases.
 // Row subtiles past a tile's valid rows are compiled out (the loop is
 // instantiated per subtile count 1..4), so a short tile costs only its own
-// MFMAs and copies.
+// MFMAs and copies, and its smaller stages let the same LDS hold more of
+// them: a one-subtile tile, whose weights stream from HBM for few rows,
+// keeps four groups of copies in flight instead of two.
 //
 // K order inside a group is free as long as A and B agree: lane half h
 // supplies group elements 32h + 8kk .. +7 at k-step kk -- word kk of the
@@ -54,25 +62,33 @@ using namespace qmoe_gemm;
 constexpr int kBM = kTileRows;
 constexpr int kWaves = 4;
 constexpr int kBN = 64 * kWaves;
-constexpr int kStages = 3;
 static_assert(kThreads == 64 * kWaves, "four waves per block");
 
-// Stage layout (bytes).  TILED: one scale|bias word per column; MLX layout:
-// a scale pair and a bias pair (two groups) per column.
-template <bool TILED>
+// Stage layout (bytes) for a tile of MSUB row subtiles: A holds MSUB x 32
+// activation rows of 128 bytes, B the four waves' codes, S their scales and
+// biases (TILED: one scale|bias word per column; MLX layout: a scale pair and
+// a bias pair, two groups, per column).  The block's LDS is sized for three
+// stages of a full tile; a shorter tile fits more stages into it, and keeps
+// that many groups of copies in flight (5 at one subtile, 4 at two).
+template <bool TILED, int MSUB = kMaxSub>
 struct Cfg {
   static constexpr int kAOff = 0;
-  static constexpr int kABytes = kBM * 128;
+  static constexpr int kABytes = MSUB * 32 * 128;
   static constexpr int kBOff = kAOff + kABytes;
   static constexpr int kBBytes = kWaves * 2 * 64 * 16;  // [wave][subtile][lane] x 16 B
   static constexpr int kSOff = kBOff + kBBytes;
   static constexpr int kSBytes = kWaves * (TILED ? 1 : 2) * 64 * 4;
   static constexpr int kStageBytes = kSOff + kSBytes;
-  static constexpr int kLdsBytes = kStages * kStageBytes;
+  static constexpr int kLdsBytes = 3 * (kMaxSub * 32 * 128 + kBBytes + kSBytes);
+  static constexpr int kStages = kLdsBytes / kStageBytes > 5 ? 5 : kLdsBytes / kStageBytes;
+  static_assert(kStages >= 3, "at least three stages");
   static_assert(kBlocksPerCU * (kLdsBytes + 4 * kMaxOrder) <= 160 * 1024, "LDS per CU");
   // copies per wave and group besides A: two code chunks, one (tiled) or two
   // (scale pair, bias pair) scale copies
   static constexpr int kOtherCopies = 2 + (TILED ? 1 : 2);
+  static constexpr int kCopies = MSUB + kOtherCopies;  // per wave and group
+  // at most 63 vector-memory operations outstanding per wave
+  static_assert((kStages - 1) * kCopies <= 63, "vmcnt range");
 };
 
 struct GemmArgs {
@@ -112,11 +128,13 @@ template <bool TILED>
 struct Ctx {
   // per-lane global sources at group 0 (advance per group)
   const char* a_src[kMaxSub];  // activation 16-byte unit of the lane's row in A copy q
-  const char* b_src[2];        // codes of the lane's column in each subtile
-  const char* s_src;           // MLX layout: scale pair (groups 2j, 2j+1) of column (wave*64 + lane);
-                               // tile layout: scale|bias word of that column
-  const char* z_src;           // MLX layout: bias pair
-  uint32_t lds;                // LDS address of the ring
+  // weight side: wave-uniform bases at group 0 and per-lane byte offsets
+  const char* b_base;  // codes of the wave's 64 columns
+  const char* s_base;  // MLX layout: scale pairs; tile layout: scale|bias words
+  const char* z_base;  // MLX layout: bias pairs
+  uint32_t b_off[2];   // the lane's code bytes in each 32-column subtile
+  uint32_t s_off;      // the lane's column's scales (and biases)
+  uint32_t lds;        // LDS address of the ring
   int G;
   int wave, lane, l32, h;
 };
@@ -126,8 +144,8 @@ struct Ctx {
 // then the two code chunks, then the scales and biases.
 template <bool TILED, int MSUB>
 __device__ __forceinline__ void issue_copy(const Ctx<TILED>& c, int g, int d) {
-  using C = Cfg<TILED>;
-  const uint32_t st = c.lds + (uint32_t)(g % kStages) * C::kStageBytes;
+  using C = Cfg<TILED, MSUB>;
+  const uint32_t st = c.lds + (uint32_t)(g % C::kStages) * C::kStageBytes;
   if (d < MSUB) {
     dma16(c.a_src[d] + (size_t)g * 128, st + C::kAOff + (uint32_t)(d * kWaves + c.wave) * 1024);
     return;
@@ -136,19 +154,19 @@ __device__ __forceinline__ void issue_copy(const Ctx<TILED>& c, int g, int d) {
   const uint32_t bdst = st + C::kBOff + (uint32_t)c.wave * 2048;
   if constexpr (TILED) {
     // one 2 KiB code chunk and one 256-byte scale|bias chunk per group
-    if (j < 2) dma16(c.b_src[j] + (size_t)g * 2048, bdst + j * 1024);
-    else dma4(c.s_src + (size_t)g * 256, st + C::kSOff + c.wave * 256);
+    if (j < 2) dma16s(c.b_base + (size_t)g * 2048 + j * 1024, c.b_off[0], bdst + j * 1024);
+    else dma4s(c.s_base + (size_t)g * 256, c.s_off, st + C::kSOff + c.wave * 256);
   } else {
-    if (j < 2) dma16(c.b_src[j] + (size_t)g * 32, bdst + j * 1024);
-    else if (j == 2) dma4(c.s_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.wave * 512);
-    else dma4(c.z_src + (size_t)(g >> 1) * 4, st + C::kSOff + c.wave * 512 + 256);
+    if (j < 2) dma16s(c.b_base + (size_t)g * 32, c.b_off[j], bdst + j * 1024);
+    else if (j == 2) dma4s(c.s_base + (size_t)(g >> 1) * 4, c.s_off, st + C::kSOff + c.wave * 512);
+    else dma4s(c.z_base + (size_t)(g >> 1) * 4, c.s_off, st + C::kSOff + c.wave * 512 + 256);
   }
 }
 
 template <bool TILED, int MSUB>
 __device__ __forceinline__ void issue_group(const Ctx<TILED>& c, int g) {
 #pragma unroll
-  for (int d = 0; d < MSUB + Cfg<TILED>::kOtherCopies; ++d) issue_copy<TILED, MSUB>(c, g, d);
+  for (int d = 0; d < Cfg<TILED, MSUB>::kCopies; ++d) issue_copy<TILED, MSUB>(c, g, d);
 }
 
 // Operands of one k-step: the wave's two dequantised weight fragments and the
@@ -164,13 +182,21 @@ struct Frag {
 // uses them, so the conversion does not wait on LDS ahead of the MFMAs).
 struct WState {
   uint32_t w[2][4];
-  uint32_t sraw[2], zraw[2];  // words holding column j's scale and bias as bf16 halves
-  int s_sh, z_sh;             // bit offset of the scale / bias half (0 or 16)
+  float s24[2], s20[2], z[2];  // column j's scale times 2^24 and 2^20 (exact), its bias
 };
 
-template <bool TILED>
+// Scale and bias of column j from the words holding them as bf16 halves at
+// bit offsets s_sh and z_sh.
+__device__ __forceinline__ void set_scale(WState& ws, int j, uint32_t sraw, uint32_t zraw, int s_sh, int z_sh) {
+  const float sc = __uint_as_float((sraw >> s_sh) << 16);
+  ws.s24[j] = sc * 16777216.0f;
+  ws.s20[j] = sc * 1048576.0f;
+  ws.z[j] = __uint_as_float((zraw >> z_sh) << 16);
+}
+
+template <bool TILED, int MSUB>
 __device__ __forceinline__ WState load_wstate(const Ctx<TILED>& c, const char* st, int g) {
-  using C = Cfg<TILED>;
+  using C = Cfg<TILED, MSUB>;
   WState ws;
   const uint4 raw0 = *reinterpret_cast<const uint4*>(st + C::kBOff + c.wave * 2048 + c.lane * 16);
   const uint4 raw1 = *reinterpret_cast<const uint4*>(st + C::kBOff + c.wave * 2048 + 1024 + c.lane * 16);
@@ -180,18 +206,15 @@ __device__ __forceinline__ WState load_wstate(const Ctx<TILED>& c, const char* s
     // one word per column: scale in the low half, bias in the high half
     const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.wave * 256);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) ws.sraw[j] = ws.zraw[j] = sw[c.l32 + 32 * j];
-    ws.s_sh = 0;
-    ws.z_sh = 16;
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t v = sw[c.l32 + 32 * j];
+      set_scale(ws, j, v, v, 0, 16);
+    }
   } else {
     // scale pair and bias pair of groups (2m, 2m+1): group g in half g & 1
     const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + C::kSOff + c.wave * 512);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      ws.sraw[j] = sw[c.l32 + 32 * j];
-      ws.zraw[j] = sw[64 + c.l32 + 32 * j];
-    }
-    ws.s_sh = ws.z_sh = (g & 1) * 16;
+    for (int j = 0; j < 2; ++j) set_scale(ws, j, sw[c.l32 + 32 * j], sw[64 + c.l32 + 32 * j], (g & 1) * 16, (g & 1) * 16);
   }
   return ws;
 }
@@ -203,83 +226,130 @@ __device__ __forceinline__ void read_a(Frag<MSUB>& f, const char* abuf, int kk, 
   for (int i = 0; i < MSUB; ++i) f.a[i] = *reinterpret_cast<const i32x4_t*>(abuf + (32 * i + l32) * 128 + unit * 16);
 }
 
-// Dword d = q % 4 of the dequantised fragment of code word j = q / 4 at
-// k-step kk: bf16_rne(fmaf(code, s, b)) of the word's codes 2d and 2d + 1,
-// low half first (k order).  The word's codes sit at bits 4t..4t+3; masking keeps two of
-// them in the low bits of the 16-bit halves, where they read as fp16
-// denormals: code 0 | 4 as q * 2^-24 (bits 0..3 of each half), code 1 | 5 as
-// q * 2^-20 (bits 4..7); shifting the word by 8 first gives codes 2 | 6 and
-// 3 | 7.  d & 2 selects the high halves (codes 4..7).
-__device__ __forceinline__ void dequant_piece(i32x4_t (&b)[2], const WState& ws, int kk, int q) {
-  const int j = q >> 2, d = q & 3;
-  const float sc = __uint_as_float((ws.sraw[j] >> ws.s_sh) << 16);
-  const float s24 = sc * 16777216.0f, s20 = sc * 1048576.0f;  // exact
-  const float z = __uint_as_float((ws.zraw[j] >> ws.z_sh) << 16);
-  const uint32_t v = (d & 1) ? ws.w[j][kk] >> 8 : ws.w[j][kk];
+// Dwords odd and odd + 2 of the dequantised fragment of code word j at
+// k-step kk (pair pr = 2j + odd): bf16_rne(fmaf(code, s, b)) of the word's
+// codes (2d, 2d + 1) for dword d, low half first (k order).  The word's codes
+// sit at bits 4t..4t+3; masking keeps two of them in the low bits of the
+// 16-bit halves, where they read as fp16 denormals: code 0 | 4 as
+// q * 2^-24 (bits 0..3 of each half), code 1 | 5 as q * 2^-20 (bits 4..7);
+// shifting the word by 8 first (odd) gives codes 2 | 6 and 3 | 7.  The low
+// halves make dword odd, the high halves (codes 4..7) dword odd + 2, from
+// the same two masked words.
+__device__ __forceinline__ void dequant_pair(i32x4_t (&b)[2], const WState& ws, int kk, int pr) {
+  const int j = pr >> 1, odd = pr & 1;
+  const float s24 = ws.s24[j], s20 = ws.s20[j], z = ws.z[j];
+  const uint32_t v = odd ? ws.w[j][kk] >> 8 : ws.w[j][kk];
   const uint32_t lo = v & 0x000F000Fu, hi = v & 0x00F000F0u;
-  if (d & 2)
-    b[j][d] = (int)cvt_pk_bf16(fma_mix<true>(lo, s24, z), fma_mix<true>(hi, s20, z));
-  else
-    b[j][d] = (int)cvt_pk_bf16(fma_mix<false>(lo, s24, z), fma_mix<false>(hi, s20, z));
+  b[j][odd] = (int)cvt_pk_bf16(fma_mix<false>(lo, s24, z), fma_mix<false>(hi, s20, z));
+  b[j][odd | 2] = (int)cvt_pk_bf16(fma_mix<true>(lo, s24, z), fma_mix<true>(hi, s20, z));
 }
 
-// One k-step: the activation fragments are read and the weight fragment
-// dequantised, then the MFMAs run in MSUB slots of two, slot p carrying the
-// copies d of group cg whose place among the group's 4 * MSUB slots is
-// 4 * kk + p... spread evenly: a scheduling barrier after every slot keeps the
-// copies trickling out between MFMAs instead of stalling the wave in a burst.
-// Latency is hidden by the other block on the CU (two blocks per CU).
-template <bool TILED, int MSUB, bool COPY>
-__device__ __forceinline__ void step(const Ctx<TILED>& c, const WState& ws, const char* abuf, int kk, int cg,
-                                     f32x16_t (&acc)[kMaxSub][2]) {
-  constexpr int D = MSUB + Cfg<TILED>::kOtherCopies;
-  constexpr int kSlots = 4 * MSUB;
-  Frag<MSUB> f;
-  read_a<MSUB>(f, abuf, kk, c.l32, c.h);
+// One MFMA slot of a k-step: subtile pair (p, j) = (s / 2, s % 2).
+template <int MSUB>
+__device__ __forceinline__ void mfma_slot(const Frag<MSUB>& f, int s, f32x16_t (&acc)[kMaxSub][2]) {
+  const int p = s >> 1, j = s & 1;
+  acc[p][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.b[j]),
+                                                      __builtin_bit_cast(bf16x8_t, f.a[p]), acc[p][j], 0, 0, 0);
+}
+
+// The MFMA slot after which dequant pair pr (0..3) of the next k-step is
+// computed.  LATE: the pairs wait for operands read at the start of the step
+// (the next group's code words), so the first two slots carry none.
+template <int MSUB, bool LATE>
+constexpr int pair_slot(int pr) {
+  constexpr int S = 2 * MSUB;
+  if constexpr (LATE) return S > 2 ? 2 + pr * (S - 2) / 4 : S - 1;
+  return pr * S / 4;
+}
+
+// One software-pipelined k-step.  The MFMAs of the current operands (cur)
+// issue one per slot; between them the wave computes the next k-step's
+// operands (nxt: its activation fragments were read at the start of the
+// step, its weight fragment is dequantised piece by piece from ws at k-step
+// kkn) and issues its share of the ring copies of group cg.  A scheduling
+// fence after every slot keeps the order, so each MFMA's matrix-core time
+// covers the vector work that follows it instead of the wave alternating a
+// dequant burst with an MFMA burst.  NEXT = false: the last k-step of the
+// tile, nothing to prepare.
+template <bool TILED, int MSUB, bool NEXT, bool LATE>
+__device__ __forceinline__ void step_pipe(const Ctx<TILED>& c, const Frag<MSUB>& cur, Frag<MSUB>& nxt,
+                                          const WState& ws, int kkn, int cg, int cstep,
+                                          f32x16_t (&acc)[kMaxSub][2]) {
+  constexpr int D = Cfg<TILED, MSUB>::kCopies;
+  constexpr int S = 2 * MSUB;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) dequant_piece(f.b, ws, kk, q);
-  // raised issue priority for the MFMA burst: the SIMD's other wave (the
-  // second block on the CU) fills the matrix core's busy cycles with its
-  // dequant VALU instead of racing this wave into the matrix pipe
-  // (measured ~4% on the 4096-token gate_up workload)
-  __builtin_amdgcn_s_setprio(1);
+  for (int s = 0; s < S; ++s) {
+    mfma_slot<MSUB>(cur, s, acc);
+    if constexpr (NEXT) {
 #pragma unroll
-  for (int p = 0; p < MSUB; ++p) {
-    acc[p][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.b[0]),
-                                                        __builtin_bit_cast(bf16x8_t, f.a[p]), acc[p][0], 0, 0, 0);
-    acc[p][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.b[1]),
-                                                        __builtin_bit_cast(bf16x8_t, f.a[p]), acc[p][1], 0, 0, 0);
-    if constexpr (COPY) {
+      for (int pr = 0; pr < 4; ++pr)
+        if (pair_slot<MSUB, LATE>(pr) == s) dequant_pair(nxt.b, ws, kkn, pr);
+    }
+    // the group's D copies spread over the 3 * S slots of k-steps 0..2
+    if (cstep >= 0) {
 #pragma unroll
       for (int d = 0; d < D; ++d)
-        if (d * kSlots / D == kk * MSUB + p) issue_copy<TILED, MSUB>(c, cg, d);
+        if (d * 3 * S / D == cstep * S + s) issue_copy<TILED, MSUB>(c, cg, d);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __builtin_amdgcn_s_setprio(0);
 }
 
-// One tile's main loop over the K groups, a ring of kStages stages with the
-// copies of group g + 2 in flight while group g is computed.  Every
-// iteration copies a group (the last group again once the tile is exhausted
-// -- into a stage nobody reads any more), so the loop body has no branches.
+// One tile's main loop over the K groups, a ring of NS stages with the copies
+// of groups g + 1 .. g + NS - 1 in flight while group g is computed (every
+// group copies one: the last group again once the tile is exhausted, the same
+// bytes into the stage that holds them, so the loop has no branches on it).
+// The operands of k-step s are prepared during k-step s - 1.  The barrier
+// that makes group g + 1 visible therefore sits at the start of group g's
+// last k-step: past it every wave has read all of stage g % NS
+// (lgkmcnt(0) before the barrier), so the copies into that stage, issued in
+// group g + 1, cannot overtake a read.
 template <bool TILED, int MSUB>
 __device__ __forceinline__ void tile_loop(const Ctx<TILED>& c, const char* smem, f32x16_t (&acc)[kMaxSub][2]) {
-  using C = Cfg<TILED>;
-  constexpr int D = MSUB + C::kOtherCopies;  // copies per wave and group
+  using C = Cfg<TILED, MSUB>;
+  constexpr int D = C::kCopies;
+  constexpr int NS = C::kStages;
   const int G = c.G;
-  issue_group<TILED, MSUB>(c, 0);
-  issue_group<TILED, MSUB>(c, min(1, G - 1));
-  for (int g = 0; g < G; ++g) {
-    // group g's copies have landed once only group g+1's are outstanding;
-    // stage (g+2) % 3 was last read in iteration g-1, which every wave has
-    // left once past the barrier
-    wait_vmem<D>();
-    __builtin_amdgcn_s_barrier();
-    const int cg = min(g + 2, G - 1);
-    const char* st = smem + (g % kStages) * C::kStageBytes;
-    const WState ws = load_wstate<TILED>(c, st, g);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) step<TILED, MSUB, true>(c, ws, st + C::kAOff, kk, cg, acc);
+  for (int i = 0; i < NS - 1; ++i) issue_group<TILED, MSUB>(c, min(i, G - 1));
+  wait_vmem<(NS - 2) * D>();  // group 0 landed
+  __builtin_amdgcn_s_barrier();
+  Frag<MSUB> fa, fb;
+  WState ws = load_wstate<TILED, MSUB>(c, smem, 0);
+  read_a<MSUB>(fa, smem + C::kAOff, 0, c.l32, c.h);
+#pragma unroll
+  for (int pr = 0; pr < 4; ++pr) dequant_pair(fa.b, ws, 0, pr);
+  // groups 0 .. G - 2: the last k-step prepares the next group's first
+  for (int g = 0; g < G - 1; ++g) {
+    const int cg = min(g + NS - 1, G - 1);
+    const char* st = smem + (g % NS) * C::kStageBytes;
+    read_a<MSUB>(fb, st + C::kAOff, 1, c.l32, c.h);
+    step_pipe<TILED, MSUB, true, false>(c, fa, fb, ws, 1, cg, 0, acc);
+    read_a<MSUB>(fa, st + C::kAOff, 2, c.l32, c.h);
+    step_pipe<TILED, MSUB, true, false>(c, fb, fa, ws, 2, cg, 1, acc);
+    read_a<MSUB>(fb, st + C::kAOff, 3, c.l32, c.h);
+    step_pipe<TILED, MSUB, true, false>(c, fa, fb, ws, 3, cg, 2, acc);
+    // group g + 1 landed for every wave (the copies of groups g + 2 ..
+    // g + NS - 1 may be outstanding); this wave's reads of stage g % NS are
+    // complete
+    wait_vmem<(NS - 2) * D>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    const char* sn = smem + ((g + 1) % NS) * C::kStageBytes;
+    ws = load_wstate<TILED, MSUB>(c, sn, g + 1);
+    read_a<MSUB>(fa, sn + C::kAOff, 0, c.l32, c.h);
+    step_pipe<TILED, MSUB, true, true>(c, fb, fa, ws, 0, cg, -1, acc);
+  }
+  {
+    // the last group (its copies repeat it)
+    const char* st = smem + ((G - 1) % NS) * C::kStageBytes;
+    read_a<MSUB>(fb, st + C::kAOff, 1, c.l32, c.h);
+    step_pipe<TILED, MSUB, true, false>(c, fa, fb, ws, 1, G - 1, 0, acc);
+    read_a<MSUB>(fa, st + C::kAOff, 2, c.l32, c.h);
+    step_pipe<TILED, MSUB, true, false>(c, fb, fa, ws, 2, G - 1, 1, acc);
+    read_a<MSUB>(fb, st + C::kAOff, 3, c.l32, c.h);
+    step_pipe<TILED, MSUB, true, false>(c, fa, fb, ws, 3, G - 1, 2, acc);
+    step_pipe<TILED, MSUB, false, false>(c, fb, fa, ws, 0, G - 1, -1, acc);
   }
   wait_vmem<0>();  // the trailing repeat copies
 }
@@ -427,18 +497,19 @@ __device__ __forceinline__ void run_unit(const GemmArgs& a, char* smem, int tile
   if constexpr (TILED) {
     // chunk (e, c, g) of the tile layout, c = the wave's 64-column block
     const int64_t chunk0 = ((int64_t)e * (a.N / 64) + nblk * kWaves + c.wave) * G;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      c.b_src[j] = reinterpret_cast<const char*>(a.w) + (chunk0 * 2 + j) * 1024 + c.lane * 16;
-    c.s_src = reinterpret_cast<const char*>(a.sb) + chunk0 * 256 + c.lane * 4;
-    c.z_src = nullptr;
+    c.b_base = reinterpret_cast<const char*>(a.w) + uniform64(chunk0 * 2048);
+    c.b_off[0] = c.b_off[1] = (uint32_t)c.lane * 16;
+    c.s_base = reinterpret_cast<const char*>(a.sb) + uniform64(chunk0 * 256);
+    c.s_off = (uint32_t)c.lane * 4;
+    c.z_base = nullptr;
   } else {
-    const int64_t col_base = (int64_t)e * a.N + nblk * kBN + c.wave * 64;
+    const int64_t col_base = uniform64((int64_t)e * a.N + nblk * kBN + c.wave * 64);
+    c.b_base = reinterpret_cast<const char*>(a.w + col_base * KW);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      c.b_src[j] = reinterpret_cast<const char*>(a.w + (col_base + j * 32 + c.l32) * KW + c.h * 4);
-    c.s_src = reinterpret_cast<const char*>(a.s + (col_base + c.lane) * G);
-    c.z_src = reinterpret_cast<const char*>(a.b + (col_base + c.lane) * G);
+    for (int j = 0; j < 2; ++j) c.b_off[j] = (uint32_t)(((j * 32 + c.l32) * KW + c.h * 4) * 4);
+    c.s_base = reinterpret_cast<const char*>(a.s + col_base * G);
+    c.z_base = reinterpret_cast<const char*>(a.b + col_base * G);
+    c.s_off = (uint32_t)(c.lane * G * 2);
   }
 
   f32x16_t acc[kMaxSub][2];

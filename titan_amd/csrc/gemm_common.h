@@ -39,6 +39,27 @@ __device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
       : "s"(lds_base), "v"(g)
       : "memory", "m0");
 }
+// The same copies from a wave-uniform base (an SGPR pair) plus a 32-bit
+// per-lane byte offset: lane i copies from sbase + voff_i.  (No instruction
+// offset: an LDS-DMA load applies it to the LDS address as well.)
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2"
+      :
+      : "s"(lds_base), "v"(voff), "s"(sbase)
+      : "memory", "m0");
+}
+__device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, %2"
+      :
+      : "s"(lds_base), "v"(voff), "s"(sbase)
+      : "memory", "m0");
+}
 // Wait until at most N vector-memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmem() {
