@@ -144,7 +144,7 @@ def calibration_copy(dev, mib=CALIBRATION_MIB, reps=5):
 # `--traffic` measures them live (rocprofv3 children started before this
 # process touches the GPU); otherwise the committed summary supplies them.
 
-TRAFFIC_KERNEL = "qmv64_flat_kernel<1, 64>"  # the one-token decode gate_up + SwiGLU kernel (bench workload 1)
+TRAFFIC_KERNEL = "qmv64_flat_kernel<1, 64, 4>"  # the one-token decode gate_up + SwiGLU kernel (bench workload 1)
 TRAFFIC_PROFILE = ROOT / "profiles" / "qmv64_decode_gate_up.traffic.txt"
 
 
@@ -299,8 +299,8 @@ def peaks_lib():
     sigs = {"qmoe_peak_stream_read": [c_vp, ctypes.c_size_t, c_vp, c_vp],
             "qmoe_peak_mfma_bf16": [c_int, c_vp, c_vp],
             "qmoe_peak_mfma_i8": [c_int, c_vp, c_vp],
-            "qmoe_peak_launch": [c_int, c_vp],
-            "qmoe_peak_chain": [c_vp, c_int, c_int, c_vp, c_int, c_int, c_int, c_vp, c_vp]}
+            "qmoe_peak_launch": [c_int, c_int, c_vp],
+            "qmoe_peak_chain": [c_vp, c_int, c_int, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp]}
     for name, argtypes in sigs.items():
         fn = getattr(L, name)
         fn.restype = c_int
@@ -435,23 +435,27 @@ def setup_cfg1(args, dev):
         if rc != 0:
             raise RuntimeError(f"floor probe failed (code {rc})")
 
-    def mk_chain(i):
+    def mk_chain(i, wpb=1):
         w = sets[i % len(sets)][0]
         idx = idxs[i]
 
         def f():
-            check(P.qmoe_peak_chain(idx.data_ptr(), 10, E, w.data_ptr(), 1024, 1024, 8, sink.data_ptr(),
+            check(P.qmoe_peak_chain(idx.data_ptr(), 10, E, w.data_ptr(), 1024, 1024, 8, wpb, sink.data_ptr(),
                                     torch.cuda.current_stream().cuda_stream))
         return f
 
-    def launch():
-        check(P.qmoe_peak_launch(1280, torch.cuda.current_stream().cuda_stream))
+    def mk_launch(wpb):
+        def f():
+            check(P.qmoe_peak_launch(1280, wpb, torch.cuda.current_stream().cuda_stream))
+        return f
 
     return wl, [mk_mlx(i) for i in range(L)], {
-        "floor": {"launch": [launch] * L, "chain": [mk_chain(i) for i in range(L)],
+        # the same 1280 waves also in workgroups of two and four waves
+        "floor": {"launch": [mk_launch(1)] * L, "chain": [mk_chain(i) for i in range(L)],
+                  "wider": {w: ([mk_launch(w)] * L, [mk_chain(i, w) for i in range(L)]) for w in (2, 4)},
                   "chain_bytes": 1280 * 1024 + 10 * 4},
         "bytes": per_call, "flops": synth.algorithmic_flops(1), "bound": "hbm",
-        "kernel": "qmv64_flat_kernel<1, 64>", "sets": len(sets),
+        "kernel": "qmv64_flat_kernel<1, 64, 4>", "sets": len(sets),
         "cycle_bytes": L * per_call,
         "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(L)]),
         "workload": "decode gate_up gather_qmm + SwiGLU: 1 token, H=2048, E=256, top_k=10, "
@@ -791,7 +795,7 @@ def run_widths(args, dev):
         del routes, lhs, idx
     return {"workload": "decode widths: T tokens x top-10 of E=256, gate_up + SwiGLU, W [256,1024,2048] int4 g64; "
                         "decode GEMV vs route + SwiGLU grouped GEMM",
-            "kernel": "qmv64_flat_kernel<1, 64> (T = 1), qmv64_kernel<1, 0, 1, 4, 64, true, false> (T > 1) | route_* + gemm_bf16_kernel<true, true>",
+            "kernel": "qmv64_flat_kernel<1, 64, 4> (T = 1), qmv64_kernel<1, 0, 1, 4, 64, true, false> (T > 1) | route_* + gemm_bf16_kernel<true, true>",
             "widths": res}
 
 
@@ -1099,6 +1103,12 @@ def main():
             sec_c, _tc = timer(args)(fl["chain"], steps, args.warmup, dev)
             res["floor"] = {"launch_us": round(sec_l * 1e6, 3), "chain_us": round(sec_c * 1e6, 3),
                             "chain_bytes": fl["chain_bytes"]}
+            for wpb, (wl_, wc_) in fl.get("wider", {}).items():
+                sl_, _x = timer(args)(wl_, steps, args.warmup, dev)
+                sc_, _y = timer(args)(wc_, steps, args.warmup, dev)
+                res["floor"][f"waves_per_block_{wpb}"] = {"launch_us": round(sl_ * 1e6, 3),
+                                                          "chain_us": round(sc_ * 1e6, 3)}
+                del _x, _y
             del fl, _tl, _tc
         for label, ex, ex_flops in meta.get("extras", ()):
             sec_ex, _te = timer(args)(ex, steps, args.warmup, dev)

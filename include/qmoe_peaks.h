@@ -32,17 +32,19 @@ int qmoe_peak_mfma_waves(void);
 int qmoe_peak_mfma_bf16(int iters, uint32_t* sink, void* stream);
 int qmoe_peak_mfma_i8(int iters, uint32_t* sink, void* stream);
 
-/* The per-call floor of a decode step that is one launch of single-wave
- * blocks.  qmoe_peak_launch: `blocks` blocks of 64 threads that do nothing.
- * qmoe_peak_chain: slots * (rows_per_expert / rows_per_block) blocks; block
- * (slot, rb) reads ids[slot] (clamped to [0, num_experts)), then the first
- * 64 16-byte units of row rb * rows_per_block of that expert's rows in w
- * (num_experts x rows_per_expert rows of row_bytes bytes, 16-byte aligned;
- * row_bytes a multiple of 16 and at least 1024), and writes one word to
- * sink[block].  Returns 1 on arguments that break these rules. */
-int qmoe_peak_launch(int blocks, void* stream);
+/* The per-call floor of a decode step that is one launch of waves, in
+ * workgroups of waves_per_block (1, 2 or 4) waves.  qmoe_peak_launch: `waves`
+ * waves that do nothing.  qmoe_peak_chain: slots * (rows_per_expert /
+ * rows_per_block) waves; wave (slot, rb) reads ids[slot] (clamped to
+ * [0, num_experts)), then the first 64 16-byte units of row
+ * rb * rows_per_block of that expert's rows in w (num_experts x
+ * rows_per_expert rows of row_bytes bytes, 16-byte aligned; row_bytes a
+ * multiple of 16 and at least 1024), and writes one word to sink[wave].
+ * Returns 1 on arguments that break these rules (including a wave count that
+ * waves_per_block does not divide). */
+int qmoe_peak_launch(int waves, int waves_per_block, void* stream);
 int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, const void* w, int rows_per_expert,
-                    int row_bytes, int rows_per_block, uint32_t* sink, void* stream);
+                    int row_bytes, int rows_per_block, int waves_per_block, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

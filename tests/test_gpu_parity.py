@@ -794,12 +794,14 @@ def test_fused_decode_group_sizes(dev, orc, gs):
 @pytest.mark.parametrize("k,K,gs", [(10, 2048, 64), (9, 2048, 64), (10, 2048, 32), (9, 2048, 128),
                                     (10, 4096, 64), (10, 6144, 128), (9, 6144, 32), (9, 8192, 64),
                                     (10, 8192, 128)])
-def test_gate_up_one_token_flat_waves(dev, orc, k, K, gs):
+def test_gate_up_one_token_flat_waves(dev, orc, k, K, gs, monkeypatch):
     """One token's fused gate_up + SwiGLU runs on waves of five consecutive
-    (pair, index) slots (qmv64_flat_kernel: ten experts x 512 indices make 1024
-    waves, some spanning two experts; k = 9 leaves a partial last wave).  The
-    same token given twice takes the four-index waves: the first token's h must
-    match bit for bit, and both stay within the bar of the oracle."""
+    (pair, index) slots (qmv64_flat_kernel, four waves per workgroup: ten
+    experts x 512 indices make 1024 waves, some spanning two experts; k = 9
+    leaves a partial last wave and a workgroup with waves past the list).
+    QMOE_DECODE_FLAT=1 takes that kernel whatever the part's SIMD count, =0 the
+    four-index waves; the same token given twice also takes the four-index
+    waves.  All must match bit for bit and stay within the bar of the oracle."""
     say(f"gate_up one token flat waves k={k} K={K} gs={gs}")
     rng = np.random.default_rng(1000 + k + K + gs)
     E, I = (256 if K <= 4096 else 32), 512
@@ -807,10 +809,14 @@ def test_gate_up_one_token_flat_waves(dev, orc, k, K, gs):
     x = synth.bf16_bits(rng.normal(size=(1, K)).astype(np.float32))
     idx = rng.choice(E, k, replace=False).astype(np.int32)[None]
     wt, st, bt = words_t(w, dev), bf16_t(s, dev), bf16_t(b, dev)
+    monkeypatch.setenv("QMOE_DECODE_FLAT", "1")
     h1 = ops.gate_up_silu(bf16_t(x, dev), wt, st, bt, i32_t(idx, dev), group_size=gs)
+    monkeypatch.setenv("QMOE_DECODE_FLAT", "0")
+    h0 = ops.gate_up_silu(bf16_t(x, dev), wt, st, bt, i32_t(idx, dev), group_size=gs)
+    monkeypatch.delenv("QMOE_DECODE_FLAT")
     h2 = ops.gate_up_silu(bf16_t(np.repeat(x, 2, axis=0), dev), wt, st, bt, i32_t(np.repeat(idx, 2, axis=0), dev),
                           group_size=gs)
-    assert torch.equal(h1[0], h2[0]) and torch.equal(h2[0], h2[1])
+    assert torch.equal(h1, h0) and torch.equal(h1[0], h2[0]) and torch.equal(h2[0], h2[1])
     gu64, _ = orc.gather_qmm_rows(x, np.zeros(k, np.int32), idx.reshape(-1), w, s, b, group_size=gs)
     h64, _ = orc.swiglu(gu64)
     assert_close_bf16(orc, bits(h1).reshape(k, I), h64, what=f"gate_up flat k={k} K={K} gs{gs}")

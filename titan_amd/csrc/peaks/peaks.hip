@@ -106,27 +106,30 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_i8_kernel(int iters, uint32
 }
 
 // Per-call floor of a one-launch decode step, in two parts.  The launch
-// alone: single-wave blocks that do nothing.  The dependent chain: each
-// single-wave block reads its kernel arguments, then the expert id of its
-// slot, then one 16-byte unit per lane of the first weight row of its row
-// block (one row of 64 units, as the decode kernel's first row), and stores
-// one word -- the three memory round trips a decode wave cannot overlap.
-__global__ __launch_bounds__(64) void launch_probe_kernel() {}
+// alone: blocks of W waves that do nothing.  The dependent chain: each wave
+// (work item blockIdx.x * W + wave) reads its kernel arguments, then the
+// expert id of its slot, then one 16-byte unit per lane of the first weight
+// row of its row block (one row of 64 units, as the decode kernel's first
+// row), and stores one word -- the three memory round trips a decode wave
+// cannot overlap.  W = 1, 2, 4: the same waves in fewer, wider workgroups.
+template <int W>
+__global__ __launch_bounds__(64 * W) void launch_probe_kernel() {}
 
-__global__ __launch_bounds__(64) void chain_probe_kernel(const int32_t* __restrict__ ids, int blocks_per_slot,
-                                                         int num_experts, const i32x4_t* __restrict__ w,
-                                                         int64_t expert_units, int64_t block_units,
-                                                         uint32_t* __restrict__ sink) {
-  const uint32_t b = blockIdx.x;
+template <int W>
+__global__ __launch_bounds__(64 * W) void chain_probe_kernel(const int32_t* __restrict__ ids, int blocks_per_slot,
+                                                             int num_experts, const i32x4_t* __restrict__ w,
+                                                             int64_t expert_units, int64_t block_units,
+                                                             uint32_t* __restrict__ sink) {
+  const int lane = threadIdx.x % 64;
+  const uint32_t b = blockIdx.x * W + threadIdx.x / 64;  // the wave's work item
   const uint32_t slot = b / (uint32_t)blocks_per_slot;
   const uint32_t rb = b - slot * (uint32_t)blocks_per_slot;
   int e = ids[slot];
   e = min(max(e, 0), num_experts - 1);
-  const i32x4_t v = __builtin_nontemporal_load(w + (int64_t)e * expert_units + (int64_t)rb * block_units +
-                                               threadIdx.x);
+  const i32x4_t v = __builtin_nontemporal_load(w + (int64_t)e * expert_units + (int64_t)rb * block_units + lane);
   uint32_t acc = (uint32_t)(v[0] ^ v[1] ^ v[2] ^ v[3]);
   for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m, 64);
-  if (threadIdx.x == 0) sink[b] = acc;
+  if (lane == 0) sink[b] = acc;
 }
 
 int status() { return hipGetLastError() == hipSuccess ? 0 : 3; }
@@ -150,27 +153,41 @@ extern "C" int qmoe_peak_mfma_bf16(int iters, uint32_t* sink, void* stream) {
   return status();
 }
 
-extern "C" int qmoe_peak_launch(int blocks, void* stream) {
-  if (blocks <= 0) return 1;
-  launch_probe_kernel<<<dim3(blocks), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>();
+extern "C" int qmoe_peak_launch(int waves, int waves_per_block, void* stream) {
+  if (waves <= 0 || (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4) ||
+      waves % waves_per_block)
+    return 1;
+  const dim3 grid(waves / waves_per_block), block(64 * waves_per_block);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (waves_per_block == 1) launch_probe_kernel<1><<<grid, block, 0, st>>>();
+  else if (waves_per_block == 2) launch_probe_kernel<2><<<grid, block, 0, st>>>();
+  else launch_probe_kernel<4><<<grid, block, 0, st>>>();
   return status();
 }
 
 extern "C" int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, const void* w, int rows_per_expert,
-                               int row_bytes, int rows_per_block, uint32_t* sink, void* stream) {
-  // every block reads units [0, 64) of row rb * rows_per_block of its expert:
-  // in bounds when a row holds at least 64 units and the row blocks tile the rows
+                               int row_bytes, int rows_per_block, int waves_per_block, uint32_t* sink,
+                               void* stream) {
+  // every wave reads units [0, 64) of row rb * rows_per_block of its expert:
+  // in bounds when a row holds at least 64 units and the row blocks tile the
+  // rows; the waves' work items are exactly 0 .. slots * blocks_per_slot - 1
+  // when the blocks of waves_per_block waves divide them
   if (!ids || !w || !sink || slots <= 0 || num_experts <= 0 || rows_per_expert <= 0 || rows_per_block <= 0 ||
       row_bytes % 16 || row_bytes / 16 < 64 || rows_per_expert % rows_per_block ||
-      (reinterpret_cast<uintptr_t>(w) & 15))
+      (reinterpret_cast<uintptr_t>(w) & 15) ||
+      (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4))
     return 1;
   const int blocks_per_slot = rows_per_expert / rows_per_block;
+  const int64_t items = (int64_t)slots * blocks_per_slot;
+  if (items % waves_per_block || items > 0x7FFFFFFF) return 1;
   const int64_t row_units = row_bytes / 16;
-  chain_probe_kernel<<<dim3((uint32_t)slots * (uint32_t)blocks_per_slot), dim3(64), 0,
-                       reinterpret_cast<hipStream_t>(stream)>>>(ids, blocks_per_slot, num_experts,
-                                                                static_cast<const i32x4_t*>(w),
-                                                                (int64_t)rows_per_expert * row_units,
-                                                                (int64_t)rows_per_block * row_units, sink);
+  const dim3 grid((uint32_t)(items / waves_per_block)), block(64 * waves_per_block);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t eu = (int64_t)rows_per_expert * row_units, bu = (int64_t)rows_per_block * row_units;
+  const i32x4_t* wp = static_cast<const i32x4_t*>(w);
+  if (waves_per_block == 1) chain_probe_kernel<1><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
+  else if (waves_per_block == 2) chain_probe_kernel<2><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
+  else chain_probe_kernel<4><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
   return status();
 }
 

@@ -16,6 +16,8 @@
 // to the dot unit two at a time.
 #include <stdarg.h>
 
+#include <stdlib.h>
+
 #include "common.h"
 #include "topk.h"
 
@@ -576,7 +578,7 @@ __device__ __forceinline__ float reduce2(float a, float b, int lane) {
 }
 
 // Fused gate_up + SwiGLU for one token (every pair reads x row 0), flat form:
-// wave b takes the kFlatRG consecutive slots f = b*kFlatRG .. of the
+// wave item b takes the kFlatRG consecutive slots f = b*kFlatRG .. of the
 // n_pairs * n_out list (pair f / n_out, index f % n_out), so a wave may span
 // two pairs, i.e. two experts (kFlatRG <= n_out).  Ten experts x 512 indices
 // are then 1024 waves, one per SIMD of a 256-CU part, where the four-index
@@ -585,19 +587,30 @@ __device__ __forceinline__ float reduce2(float a, float b, int lane) {
 // the arithmetic is qmv64_kernel's (same loads, same chunk sums), and the fifth
 // slot's reduction follows reduce8's tree, so every output is bit-identical to
 // that kernel's.  Slots past the list repeat its last entry and are not stored.
+//
+// The waves come W to a workgroup: wave w of block b is item
+// xcd_item(b) * W + w, its lane is threadIdx.x % 64, its LDS staging its own
+// slice, and a wave past the last item leaves at once (the kernel has no
+// block-wide barrier).  Fewer, wider workgroups reach the GPU sooner: on
+// workload 1's 1280-wave shape, the dependent chain arguments -> expert id ->
+// first weight row -> store measured 2.86 us per launch in single-wave
+// workgroups and 2.42 us in four-wave ones.
 constexpr int kFlatRG = 5;
+constexpr int kFlatWaves = 4;  // waves per workgroup
 
-template <int NV, int GS>
-__global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
+template <int NV, int GS, int W>
+__global__ __launch_bounds__(64 * W) void qmv64_flat_kernel(QmvArgs a) {
   constexpr int KE = 2048 * NV;
   constexpr int G = KE / GS;            // groups per row
   constexpr int UPR = G / 8;            // 16-byte scale units per row
   constexpr int UNITS = 4 * kFlatRG * UPR;  // [slot][gate/up][scale/bias][UPR]
   constexpr int UPL = (UNITS + 63) / 64;
   constexpr int64_t KW = KE / 8;
-  __shared__ __attribute__((aligned(16))) uint16_t sbl[UNITS * 8];
+  __shared__ __attribute__((aligned(16))) uint16_t sbl_w[W][UNITS * 8];
   QMV_STAMP(ts_entry);
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x % 64;
+  const int wave = W == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x / 64));
+  uint16_t* sbl = sbl_w[wave];
   // every kernel argument the wave reads, in one batch of scalar loads (left
   // alone, the compiler spreads them over three dependent round trips)
   const uint16_t* ax = a.x;
@@ -613,11 +626,14 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
   QMV_STAMP(ts_args);
   const FastDiv bd{(uint32_t)n_out, bd_m, bd_s};  // n_out
   const uint32_t total = npairs * (uint32_t)n_out;  // < 2^31 (host)
-  // consecutive waves on one XCD (xcd_item): the scale and bias lines that
-  // two neighbouring waves split (five rows of 64 bytes each) are then fetched
-  // into one L2, once
+  // consecutive items on one XCD (xcd_item over the blocks, then the block's
+  // waves): the scale and bias lines that two neighbouring waves split (five
+  // rows of 64 bytes each) are then fetched into one L2, once
   // (the grid size from the batch above: gridDim.x would cost another dependent load)
-  const uint32_t f0 = xcd_item(blockIdx.x, (total + kFlatRG - 1) / kFlatRG) * (uint32_t)kFlatRG;
+  const uint32_t nitems = (total + kFlatRG - 1) / kFlatRG;
+  const uint32_t item = xcd_item(blockIdx.x, (nitems + W - 1) / W) * (uint32_t)W + (uint32_t)wave;
+  if (item >= nitems) return;
+  const uint32_t f0 = item * (uint32_t)kFlatRG;
   const uint32_t flast = min(f0 + (uint32_t)(kFlatRG - 1), total - 1);
   const uint32_t ra = fast_div(f0, bd);
   const uint32_t rb = fast_div(flast, bd);
@@ -743,8 +759,8 @@ __global__ __launch_bounds__(64) void qmv64_flat_kernel(QmvArgs a) {
 #ifdef QMOE_QMV_STAMPS
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   QMV_STAMP(ts_stored);
-  if (lane == 0 && blockIdx.x < kStampBlocks) {
-    uint64_t* o = qmv_stamps + (size_t)blockIdx.x * kStampsPerBlock;
+  if (lane == 0 && item < kStampBlocks) {
+    uint64_t* o = qmv_stamps + (size_t)item * kStampsPerBlock;
     o[0] = ts_entry; o[1] = ts_args; o[2] = ts_id; o[3] = ts_first; o[4] = ts_reduced; o[5] = ts_stored;
   }
 #endif
@@ -1368,20 +1384,27 @@ int simd_count() {
 // arithmetic on the busiest SIMD: waves of RG indices compute 2 * RG rows, and
 // ceil(waves / SIMDs) of them share a SIMD.  Returns -1 when the flat form does
 // not apply or is no better.
+// The one-token flat form where its shape rules hold and it puts fewer rows
+// on the busiest SIMD than the four-index waves; QMOE_DECODE_FLAT=0 turns it
+// off and QMOE_DECODE_FLAT=1 takes it wherever the shape allows (both results
+// are bit-identical; tests pin the dispatch with it).  -1: not taken.
 int launch_qmv_flat(const QmvArgs& a, hipStream_t st) {
+  const char* env = getenv("QMOE_DECODE_FLAT");
+  const int force = env && env[0] ? (env[0] == '1' ? 1 : 0) : -1;
+  if (force == 0) return -1;
   if (a.x_rows || a.n_pairs != a.x_div || a.n_out < kFlatRG || a.K % 2048) return -1;
   const int64_t total = a.n_pairs * (int64_t)a.n_out;
   if (total <= 0 || total > 0x7FFFFFFF || (int64_t)a.num_experts * a.n_w > 0x7FFFFFFF) return -1;
   const int64_t S = simd_count();
   const int64_t waves4 = a.n_pairs * ((a.n_out + QMOE_QMV_RG_GU - 1) / QMOE_QMV_RG_GU);
   const int64_t waves5 = (total + kFlatRG - 1) / kFlatRG;
-  if ((waves5 + S - 1) / S * (2 * kFlatRG) >= (waves4 + S - 1) / S * (2 * QMOE_QMV_RG_GU)) return -1;
+  if (force != 1 && (waves5 + S - 1) / S * (2 * kFlatRG) >= (waves4 + S - 1) / S * (2 * QMOE_QMV_RG_GU)) return -1;
   QmvArgs b = a;
   b.blk_div = make_fastdiv((uint32_t)a.n_out);
-  dim3 grid((unsigned)waves5), block(64);
+  dim3 grid((unsigned)((waves5 + kFlatWaves - 1) / kFlatWaves)), block(64 * kFlatWaves);
 #define QMV_FLAT(NV_, GS_) \
   if (a.K == 2048 * NV_ && a.group_size == GS_) { \
-    qmv64_flat_kernel<NV_, GS_><<<grid, block, 0, st>>>(b); \
+    qmv64_flat_kernel<NV_, GS_, kFlatWaves><<<grid, block, 0, st>>>(b); \
     return qmoe::launch_status("qmv64_flat_kernel"); \
   }
 #define QMV_FLAT_GS(NV_) QMV_FLAT(NV_, 32) QMV_FLAT(NV_, 64) QMV_FLAT(NV_, 128)
