@@ -8,10 +8,13 @@ codes + scales + biases once, plus x in and h out).  One step is one call.
 
 Method: every step reads a different weight set and a different set of 10
 experts (weight sets rotated over >= 1.2 GB so the 256 MB Infinity Cache cannot
-serve them), the K timed launches are captured in one HIP graph, and the graph
-is timed with events on the stream it is replayed on.  The other four
-workloads are measured the same way and reported under ``configs``; the CPU
-baseline is the oracle's C restatement timed on this host.
+serve them), each window of K launches is captured in one HIP graph between
+two single-wave launches that write the GPU's 100 MHz clock, and the windows'
+graphs are replayed back to back: a window's time is the difference of its two
+clock stamps, which leaves each graph's own launch outside it (events around
+the same replays, which include it, are reported beside).  The other workloads
+are measured the same way and reported under ``configs``; the CPU baseline is
+the oracle's C restatement timed on this host.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--configs 0,1,2,3,4,5,6,7]
 """
@@ -281,8 +284,88 @@ def time_graph(cycle, steps, warmup, dev, min_rounds=7):
                  "graphs": graphs}
 
 
+def time_stamped(cycle, steps, warmup, dev, min_rounds=7):
+    """Time a rotation cycle of launches in windows of exactly `steps`, from
+    the GPU's own clock.
+
+    max(min_rounds, windows) windows -- consecutive windows continue the
+    cycle, as in time_graph -- are each captured as one graph that opens and
+    closes with a single-wave stamp launch (qmoe_peak_stamp: the 100 MHz
+    s_memrealtime counter, written with a vector store), and the graphs are
+    replayed back to back.  A window's time is the difference of its two
+    stamps: its `steps` launches plus the one stamp launch that closes it.  The
+    GPU-side cost of launching each graph falls before its opening stamp,
+    outside every window (time_graph brackets each graph launch with events,
+    and that cost is then spread over the window's calls).  HIP does not time
+    events recorded by graph nodes (hipEventElapsedTime fails on them), hence
+    the stamp kernel.  After `warmup` eager launches and ~0.3 s of untimed
+    replays, the graphs are replayed once more and the stamps read.  Returns
+    (median seconds per step, {"min", "median", "max", "rounds", "windows",
+    "graphs"})."""
+    import statistics
+
+    import torch
+
+    L = len(cycle)
+    assert L % steps == 0, (L, steps)
+    windows = L // steps
+    rounds = max(min_rounds, windows)
+    for i in range(warmup):
+        cycle[i % L]()
+    torch.cuda.synchronize()
+    P = peaks_lib()
+    stamps = torch.zeros(2 * rounds, dtype=torch.int64, device=dev)
+
+    def stamp(slot, st):
+        if P.qmoe_peak_stamp(stamps.data_ptr(), slot, st) != 0:
+            raise RuntimeError("qmoe_peak_stamp failed")
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graphs = []
+    with torch.cuda.stream(s):
+        for r in range(rounds):
+            w = r % windows
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                stamp(2 * r, s.cuda_stream)
+                for fn in cycle[w * steps:(w + 1) * steps]:
+                    fn()
+                stamp(2 * r + 1, s.cuda_stream)
+            graphs.append(g)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    n_warm = min(50, max(1, int(0.3 / max(time.perf_counter() - t0, 1e-4))))
+    for _ in range(n_warm):
+        for g in graphs:
+            g.replay()
+    # the timed pass: also events around each graph launch (their span adds
+    # the graph launch to the window: both figures from the same replays)
+    st = torch.cuda.current_stream()
+    evs = []
+    for g in graphs:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    t = stamps.cpu().numpy()
+    per = [float(t[2 * r + 1] - t[2 * r]) * 1e-8 / steps for r in range(rounds)]
+    if min(per) <= 0:
+        raise RuntimeError(f"non-increasing GPU clock stamps: {t.tolist()}")
+    med = statistics.median(per)
+    ev = statistics.median([a.elapsed_time(b) / 1e3 / steps for a, b in evs])
+    return med, {"min": min(per), "median": med, "max": max(per), "rounds": rounds, "windows": windows,
+                 "graphs": graphs, "events_per_step": ev}
+
+
 def timer(args):
-    return time_eager if args.eager else time_graph
+    return time_eager if args.eager else time_stamped
 
 
 # ------------------------------------------------------------ measured peaks
@@ -300,6 +383,7 @@ def peaks_lib():
             "qmoe_peak_mfma_bf16": [c_int, c_vp, c_vp],
             "qmoe_peak_mfma_i8": [c_int, c_vp, c_vp],
             "qmoe_peak_launch": [c_int, c_int, c_vp],
+            "qmoe_peak_stamp": [c_vp, c_int, c_vp],
             "qmoe_peak_chain": [c_vp, c_int, c_int, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp]}
     for name, argtypes in sigs.items():
         fn = getattr(L, name)
@@ -1074,6 +1158,9 @@ def main():
                "us_per_call_min": round(tinfo["min"] * 1e6, 3), "us_per_call_max": round(tinfo["max"] * 1e6, 3),
                "timed_rounds": tinfo["rounds"], "steps_per_round": steps, "cycle_launches": len(cycle),
                "kernel": meta["kernel"], "weight_sets": meta["sets"]}
+        if "events_per_step" in tinfo:
+            # the same replays timed by events around each window's graph launch
+            res["us_per_call_with_graph_launch"] = round(tinfo["events_per_step"] * 1e6, 3)
         if meta["bound"] == "hbm":
             gbs = meta["bytes"] / sec / 1e9
             res.update(metric="HBM GB/s", value=round(gbs, 1), bytes_per_call=meta["bytes"],

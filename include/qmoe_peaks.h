@@ -46,6 +46,11 @@ int qmoe_peak_launch(int waves, int waves_per_block, void* stream);
 int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, const void* w, int rows_per_expert,
                     int row_bytes, int rows_per_block, int waves_per_block, uint32_t* sink, void* stream);
 
+/* One single-wave launch that writes the GPU's constant 100 MHz clock
+ * (s_memrealtime, 10 ns ticks) to stamps[slot] (slot >= 0, within the
+ * caller's buffer).  Returns 1 on a null buffer or a negative slot. */
+int qmoe_peak_stamp(uint64_t* stamps, int slot, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,6 +132,14 @@ __global__ __launch_bounds__(64 * W) void chain_probe_kernel(const int32_t* __re
   if (lane == 0) sink[b] = acc;
 }
 
+// One wave writes the GPU's constant 100 MHz clock (s_memrealtime) to
+// stamps[slot] with a vector store: placed between the timed windows of one
+// graph, it times each window from the GPU without a graph launch inside it.
+__global__ __launch_bounds__(64) void stamp_kernel(uint64_t* __restrict__ stamps, int slot) {
+  const uint64_t t = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) stamps[slot] = t;
+}
+
 int status() { return hipGetLastError() == hipSuccess ? 0 : 3; }
 
 }  // namespace
@@ -188,6 +196,12 @@ extern "C" int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, c
   if (waves_per_block == 1) chain_probe_kernel<1><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
   else if (waves_per_block == 2) chain_probe_kernel<2><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
   else chain_probe_kernel<4><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
+  return status();
+}
+
+extern "C" int qmoe_peak_stamp(uint64_t* stamps, int slot, void* stream) {
+  if (!stamps || slot < 0) return 1;
+  stamp_kernel<<<dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>(stamps, slot);
   return status();
 }
 
