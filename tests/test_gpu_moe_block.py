@@ -387,3 +387,31 @@ def test_block_decode_takes_the_topk_kernels(dev, orc):
         torch.cuda.synchronize()
         assert torch.equal(y, want), f"T={T}"
     assert not blk.decodes_with_topk(7)  # 70 pairs: the sorted path
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_block_decode_top_k_past_tile_kernels(dev, orc, T):
+    """top_k = 20 is past the tile-layout down kernel's 16 experts per token
+    (qmoe_moe_down_wsum_tiles), so the block keeps the MLX tensors resident
+    and decodes from them (qmoe_moe_down_wsum takes up to 64); at T * k < 64
+    the call is a decode and must meet the oracle's bar."""
+    E, H, I, k = 64, 2048, 512, 20
+    say(f"MoE block decode top_k={k} T={T}")
+    gu, dn, router, _ = _block_problem(40 + T, E, H, I)
+    rng = np.random.default_rng(60 + T)
+    x = synth.bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
+    blk = moe_block.SparseMoeBlock(bf16_t(router, dev), _dev_w(gu, dev), _dev_w(dn, dev), k)
+    assert not moe_block.tile_decode_supported(H, I, top_k=k)
+    assert not blk.decode_tiles and blk.gate_up is not None and blk.down is not None
+    assert T * k < blk.sort_min_pairs and not blk.decodes_with_topk(T)
+    xt = bf16_t(x, dev)
+    y = bits(blk(xt))
+    idx, sc = blk.route(xt)
+    ridx = idx.cpu().numpy()
+    tok = np.repeat(np.arange(T), k).astype(np.int32)
+    gu64, _ = orc.gather_qmm_rows(x, tok, ridx.reshape(-1), *gu)
+    _, h16 = orc.swiglu(gu64)
+    y64, _ = orc.down_wsum(h16.reshape(T, k, I), ridx, sc.cpu().numpy(), *dn)
+    rep = orc.err_report(y, y64)
+    print(f"[parity] block decode top_k={k} T={T}: {rep}", flush=True)
+    assert rep["rel_to_max"] <= 2.0 ** -7

@@ -89,3 +89,56 @@ def test_cache_switch(monkeypatch):
     assert not prepared.enabled()
     monkeypatch.setenv("TITAN_AMD_TILE_CACHE", "1")
     assert prepared.enabled()
+
+
+def test_lookup_never_builds(builds):
+    w, s, b = _trio()
+    assert prepared.lookup(w, s, b) is None and len(builds) == 0
+    a = prepared.tile_weights(w, s, b)
+    assert prepared.lookup(w, s, b) is a and len(builds) == 1
+    s.add_(1)
+    assert prepared.lookup(w, s, b) is None and len(builds) == 1
+
+
+class _Tiles:
+    tile_rows = 128
+    num_experts = 2
+    rows = 64
+
+
+def _dispatch_spy(monkeypatch, mod, names):
+    seen = []
+    for n in names:
+        monkeypatch.setattr(mod.ops, n, lambda *a, _n=n, **k: (seen.append(_n), torch.zeros(64, 256))[1])
+    monkeypatch.setattr(mod.ops, "tile_rows", lambda: 128)
+    return seen
+
+
+@pytest.mark.parametrize("cache", ["1", "0"])
+def test_grouped_gemm_ops_read_only_prepared_copies(builds, monkeypatch, cache):
+    """The bf16 and int8 grouped-GEMM ops take the tile-layout kernel only for a
+    tensor prepared ahead of time (warmup), and the MLX-layout kernel
+    otherwise -- no repack is built inside a call, and none at all with
+    TITAN_AMD_TILE_CACHE=0."""
+    from titan_amd.kernels import moe_gather_int8, moe_gather_ws
+
+    monkeypatch.setenv("TITAN_AMD_TILE_CACHE", cache)
+    w, s, b = _trio(E=2, N=256, K=128)
+    x = torch.zeros(64, 1, 128, dtype=torch.bfloat16)
+    ids = torch.zeros(64, dtype=torch.int32)
+    seen = _dispatch_spy(monkeypatch, moe_gather_ws, ["gather_qmm_sorted", "gather_qmm_sorted_tiles"])
+    moe_gather_ws.hip(x, w, s, b, ids, _Tiles())
+    assert seen == ["gather_qmm_sorted"] and len(builds) == 0
+    seen8 = _dispatch_spy(monkeypatch, moe_gather_int8, ["gather_qmm_int8_sorted", "gather_qmm_int8_sorted_tiles"])
+    monkeypatch.setattr(moe_gather_int8, "quantize_activations", lambda x: (x, x))
+    moe_gather_int8.hip(x, w, s, b, ids, None, _Tiles())
+    assert seen8 == ["gather_qmm_int8_sorted"] and len(builds) == 0
+    # prepared ahead of time (what warmup does): both ops read the copy
+    tabs = moe_gather_int8.build_tables(w, s, b)
+    assert len(builds) == (1 if cache == "1" else 0) and (tabs.tw is None) == (cache == "0")
+    moe_gather_ws.hip(x, w, s, b, ids, _Tiles())
+    moe_gather_int8.hip(x, w, s, b, ids, None, _Tiles())
+    tiled = cache == "1"
+    assert seen[-1] == ("gather_qmm_sorted_tiles" if tiled else "gather_qmm_sorted")
+    assert seen8[-1] == ("gather_qmm_int8_sorted_tiles" if tiled else "gather_qmm_int8_sorted")
+    assert len(builds) == (1 if tiled else 0)

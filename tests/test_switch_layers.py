@@ -119,3 +119,35 @@ def test_custom_activation_gets_up_then_gate(orc):
     # the default module computes silu(gate) * up from that order
     g, u = up_then_gate[0], up_then_gate[1]
     assert torch.equal(SwiGLU()(u, g), swiglu(g, u))
+
+
+def test_passing_the_swiglu_function_matches_the_default(orc):
+    """The bare swiglu function takes (gate, x); given as the activation it is
+    wrapped in the SwiGLU module (called with (x_up, x_gate)), so the layer
+    computes silu(gate) * up either way."""
+    rng = np.random.default_rng(5)
+    E, K, I, k = 4, 128, 64, 2
+    gu, gu_layer = _layer(orc, rng, E, 2 * I, K)
+    dn, dn_layer = _layer(orc, rng, E, K, I)
+    x = bf16_t(orc.bf16_from_f32(rng.normal(size=(3, K)).astype(np.float32)))
+    ids = torch.tensor([[0, 1], [2, 3], [1, 2]])
+    want = SwitchGLU(dn_layer, gate_up_proj=gu_layer)(x, ids)
+    got = SwitchGLU(dn_layer, gate_up_proj=gu_layer, activation=swiglu)(x, ids)
+    assert torch.equal(got, want)
+
+
+def test_tile_decode_envelope_includes_top_k():
+    """The block decodes from its one tile-layout copy only where the tile
+    decode kernels take the shape: hidden 2048 n (n <= 4), intermediate 512,
+    group 64 4-bit codes and at most 16 experts per token
+    (qmoe_moe_down_wsum_tiles); otherwise it keeps the MLX tensors."""
+    from titan_amd.moe_block import TILE_DECODE_MAX_K, tile_decode_supported
+
+    assert TILE_DECODE_MAX_K == 16
+    assert tile_decode_supported(2048, 512, top_k=10)
+    assert tile_decode_supported(8192, 512, top_k=16)
+    assert not tile_decode_supported(2048, 512, top_k=17)
+    assert not tile_decode_supported(2048, 512, top_k=20)
+    assert not tile_decode_supported(2560, 512, top_k=8)
+    assert not tile_decode_supported(2048, 768, top_k=8)
+    assert not tile_decode_supported(2048, 512, group_size=32, top_k=8)

@@ -43,23 +43,26 @@ class Int8Tables:
     reference's tables add 18.8% of the weights (transposed scales, folded
     bias, nibble sums); these are a permuted copy of the weights themselves,
     shared with the bf16 path through the prepared cache.  Passing them is the
-    caller's opt-in to the approximate path."""
+    caller's opt-in to the approximate path.  ``tw`` None (the tile cache off,
+    ``TITAN_AMD_TILE_CACHE=0``): the MLX-layout int8 kernel reads the tensors
+    as they are."""
 
-    tw: ops.TileWeights
+    tw: ops.TileWeights | None
 
     @property
     def nbytes(self) -> int:
-        return self.tw.nbytes
+        return 0 if self.tw is None else self.tw.nbytes
 
 
 def build_tables(wq, scales, biases) -> Int8Tables:
     """One weight tensor's tables: its tile-layout repack, built once per tensor
-    (cached by the tensors' identity, :mod:`.prepared`)."""
+    (cached by the tensors' identity, :mod:`.prepared`); none with the tile
+    cache off."""
     if wq.dim() != 3 or scales.shape != biases.shape or scales.dim() != 3:
         raise ValueError("expected w [E, N, K/8] and scales/biases [E, N, K/64]")
     if wq.shape[-1] * 8 != scales.shape[-1] * GROUP:
         raise ValueError("w and scales disagree on K")
-    return Int8Tables(prepared.tile_weights(wq, scales, biases))
+    return Int8Tables(prepared.tile_weights(wq, scales, biases) if prepared.enabled() else None)
 
 
 def pick_cfg(N: int):
@@ -79,19 +82,24 @@ def reference(x, wq, scales, biases, rhs_indices, tables=None, tiles=None, *, gr
 
 def hip(x, wq, scales, biases, rhs_indices, tables=None, tiles=None, *, group_size=GROUP, bits=BITS):
     """Quantise the rows, then the int8 grouped GEMM.  Same signature as
-    :func:`reference`; ``tables`` None builds them for this call."""
+    :func:`reference`; ``tables`` None takes the tensor's prepared copy when
+    one was built (``warmup``), else the MLX-layout kernel (nothing is built
+    here)."""
     E, N = int(wq.shape[0]), int(scales.shape[1])
     if pick_cfg(N) is None:
         raise ops.QmoeUnsupported(ops._lib.ERR_UNSUPPORTED, f"no int8 tiling for N = {N}")
     if tables is None:
-        tables = build_tables(wq, scales, biases)
+        tables = Int8Tables(prepared.lookup(wq, scales, biases) if prepared.enabled() else None)
     R, K = int(x.shape[0]), int(x.shape[-1])
     if tiles is None:
         tiles = build_tiles(rhs_indices, E)
     if tiles.tile_rows != ops.tile_rows() or tiles.num_experts != E or tiles.rows != R:
         raise ValueError("tile table does not match this call")
     xi, sx = quantize_activations(x.reshape(R, K))
-    y = ops.gather_qmm_int8_sorted_tiles(xi, sx, tables.tw, tiles)
+    if tables.tw is not None:
+        y = ops.gather_qmm_int8_sorted_tiles(xi, sx, tables.tw, tiles)
+    else:
+        y = ops.gather_qmm_int8_sorted(xi, sx, wq, scales, biases, tiles, None, group_size, bits)
     return y.reshape(R, 1, N)
 
 

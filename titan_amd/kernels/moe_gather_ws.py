@@ -6,10 +6,10 @@ The weights of a (tile, column block) are dequantised in registers as
 ``bf16_rne(fmaf(q, s, b))`` (moe_gather_ws.py:343-344) and fed to
 ``v_mfma_f32_32x32x16_bf16``; rows are tiled raggedly per expert through the
 caller-owned :class:`TileTable` (moe_gather_ws.py:159-202).  The weight tensor
-is read in the tile layout, repacked once per tensor and kept
-(:mod:`.prepared`, filled ahead of time by the patches' ``warmup``); with
-that cache off, the MLX-layout kernel reads the tensors as they are (the same
-bits, ~20% slower).
+is read in the tile layout when a repack of it was prepared ahead of time
+(:mod:`.prepared`, filled by the patches' ``warmup``); otherwise -- no
+warmup, or ``TITAN_AMD_TILE_CACHE=0`` -- the MLX-layout kernel reads the
+tensors as they are (the same bits, ~20% slower).  A call builds nothing.
 
 Exactness: the reference holds its Metal kernel bit-identical to MLX's own
 sorted gather.  Here the bar is at most one bf16 ULP on live elements against
@@ -66,8 +66,8 @@ def hip(x, wq, scales, biases, rhs_indices, tiles=None, *, group_size=GROUP, bit
         tiles = build_tiles(rhs_indices, E)
     if tiles.tile_rows != ops.tile_rows() or tiles.num_experts != E or tiles.rows != R:
         raise ValueError("tile table does not match this call")
-    if prepared.enabled():
-        tw = prepared.tile_weights(wq, scales, biases)
+    tw = prepared.lookup(wq, scales, biases) if prepared.enabled() else None
+    if tw is not None:
         y = ops.gather_qmm_sorted_tiles(x.reshape(R, K), tw, tiles)
     else:
         y = ops.gather_qmm_sorted(x.reshape(R, K), wq, scales, biases, tiles, None, group_size, bits)

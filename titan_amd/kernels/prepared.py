@@ -24,11 +24,11 @@ import torch
 
 from .. import ops
 
-__all__ = ["tile_weights", "enabled", "clear_cache", "stats", "nbytes"]
+__all__ = ["tile_weights", "lookup", "enabled", "clear_cache", "stats", "nbytes"]
 
 _lock = threading.RLock()  # re-entrant: a weakref callback may run while it is held
 _PREP: dict = {}
-_STATS = {"built": 0, "hits": 0}
+_STATS = {"built": 0, "hits": 0, "misses": 0}
 
 
 def enabled() -> bool:
@@ -39,9 +39,10 @@ def _key(w, scales, biases, swiglu_pairs):
     return (id(w), id(scales), id(biases), tuple(w.shape), bool(swiglu_pairs))
 
 
-def tile_weights(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
-                 swiglu_pairs: bool = False) -> ops.TileWeights:
-    """The tile-layout repack of (w, scales, biases), built on first use."""
+def lookup(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
+           swiglu_pairs: bool = False):
+    """The prepared tile-layout copy of (w, scales, biases), or None when none
+    was built for these tensors as they are now (nothing is built here)."""
     key = _key(w, scales, biases, swiglu_pairs)
     versions = (w._version, scales._version, biases._version)
     with _lock:
@@ -51,6 +52,19 @@ def tile_weights(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
             if all(r() is t for r, t in zip(refs, (w, scales, biases))) and ver == versions:
                 _STATS["hits"] += 1
                 return tw
+        _STATS["misses"] += 1
+    return None
+
+
+def tile_weights(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
+                 swiglu_pairs: bool = False) -> ops.TileWeights:
+    """The tile-layout repack of (w, scales, biases): the cached copy, or a new
+    one built and kept."""
+    tw = lookup(w, scales, biases, swiglu_pairs=swiglu_pairs)
+    if tw is not None:
+        return tw
+    key = _key(w, scales, biases, swiglu_pairs)
+    versions = (w._version, scales._version, biases._version)
     tw = ops.repack_tiles(w, scales, biases, swiglu_pairs=swiglu_pairs)
 
     def _drop(_ref, key=key):

@@ -37,7 +37,7 @@ experts, hidden 2048: gate_up 5.7 against 5.0 us, down at 8 tokens 14.4
 against 11.1 us), so ``resident="both"`` keeps the MLX tensors too and
 decodes from them, at twice the memory.  Shapes outside the tile-layout
 decode kernels' envelope (hidden a multiple of 2048 up to 8192, intermediate
-512) keep the MLX tensors for decode either way.
+512, top-k up to 16) keep the MLX tensors for decode either way.
 """
 
 from __future__ import annotations
@@ -48,7 +48,8 @@ import torch
 
 from . import ops
 
-__all__ = ["SparseMoeBlock", "SharedExpert", "DECODE_MAX_PAIRS", "ROUTER_GEMV_MAX_T", "tile_decode_supported"]
+__all__ = ["SparseMoeBlock", "SharedExpert", "DECODE_MAX_PAIRS", "ROUTER_GEMV_MAX_T", "TILE_DECODE_MAX_K",
+           "tile_decode_supported"]
 
 # switch_layers.py:218: SwitchGLU sorts when indices.size >= 64
 DECODE_MAX_PAIRS = 64
@@ -58,10 +59,17 @@ DECODE_MAX_PAIRS = 64
 ROUTER_GEMV_MAX_T = 16
 
 
-def tile_decode_supported(hidden: int, inter: int, group_size: int = ops.GROUP, bits: int = ops.BITS) -> bool:
+# qmoe_moe_down_wsum_tiles takes at most this many experts per token (the
+# MLX-layout qmoe_moe_down_wsum takes up to 64)
+TILE_DECODE_MAX_K = 16
+
+
+def tile_decode_supported(hidden: int, inter: int, group_size: int = ops.GROUP, bits: int = ops.BITS,
+                          top_k: int = 1) -> bool:
     """Do the tile-layout decode kernels (qmoe_moe_gate_up_swiglu_tiles,
-    qmoe_moe_down_wsum_tiles) take a SwiGLU MLP of this shape?"""
-    return (group_size, bits) == (ops.GROUP, ops.BITS) and hidden % 2048 == 0 and hidden <= 8192 and inter == 512
+    qmoe_moe_down_wsum_tiles) take a SwiGLU MLP of this shape and top-k?"""
+    return ((group_size, bits) == (ops.GROUP, ops.BITS) and hidden % 2048 == 0 and hidden <= 8192
+            and inter == 512 and 1 <= top_k <= TILE_DECODE_MAX_K)
 
 
 @dataclass
@@ -127,7 +135,7 @@ class SparseMoeBlock:
         # decode from the same tile-layout copy when its kernels take the shape;
         # the MLX tensors stay resident only when something still reads them
         self.decode_tiles = self.resident == "tiles" and tile_decode_supported(self.hidden, self.intermediate,
-                                                                               group_size, bits)
+                                                                               group_size, bits, self.top_k)
         self.gate_up = None if self.decode_tiles else tuple(gate_up)
         self.down = None if self.decode_tiles else tuple(down)
         # the sorted (grouped GEMM) path from this many (token, expert) pairs
@@ -216,7 +224,7 @@ class SparseMoeBlock:
         to the down kernel (qmoe_moe_gate_up_swiglu_tiles_topk: one launch
         fewer than router_topk + the decode kernels, same results)?"""
         return (self.decode_tiles and T <= 16 and T * self.top_k < self.sort_min_pairs
-                and self.top_k <= 16 and self.num_experts <= 1024)
+                and self.num_experts <= 1024)
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         H = x.shape[-1]

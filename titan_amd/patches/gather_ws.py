@@ -15,10 +15,13 @@ on top and takes what it wants first.
     TITAN_AMD_MOE_GATHER_WS_MIN_TOKENS=7 token floor (7 tokens x top-10 = the 64-row sort threshold)
     TITAN_AMD_MOE_GATHER_WS_MIN_ROWS=64  routed-row floor when the token count is unknown
 
-Memory: each routed weight tensor's tile-layout repack, as large as the tensor,
-built on its first call or by ``warmup(model)`` and shared with the int8
-overlay (``TITAN_AMD_TILE_CACHE=0``: none; the MLX-layout kernel runs).  The
-tile table is built per call or passed by the caller.
+Memory: none by default, as the reference's overlay: a call reads the
+tensors as they are (the MLX-layout kernel) unless ``warmup(model)`` has
+repacked them into the tile layout (one copy per routed weight tensor, as
+large as the tensor, shared with the int8 overlay; ~20% faster).  A call
+never builds a repack, so it allocates nothing beyond its output and tile
+table and can be captured in a graph.  ``TITAN_AMD_TILE_CACHE=0``: warmup
+prepares nothing.  The tile table is built per call or passed by the caller.
 """
 
 from __future__ import annotations

@@ -13,9 +13,11 @@ Everything else falls through to what was installed before.
     TITAN_AMD_MOE_INT8_SKIP_DOWN=1      leave projections with K <= 1024 (the down
                                         projection) to the layers below
 
-Memory: each routed weight tensor's tile-layout repack (:class:`Int8Tables`),
-as large as the tensor and shared with the bf16 overlay; ``warmup(model)``
-builds them ahead of the first prefill.
+Memory: none unless ``warmup(model)`` builds each routed weight tensor's
+tile-layout repack (:class:`Int8Tables`, as large as the tensor and shared
+with the bf16 overlay) ahead of the first prefill; without it the MLX-layout
+int8 kernel reads the tensors as they are.  A call builds nothing.
+``TITAN_AMD_TILE_CACHE=0``: warmup prepares nothing.
 """
 
 from __future__ import annotations
@@ -97,7 +99,9 @@ def clear_cache() -> None:
 def warmup(model=None) -> int:
     """Build the tables of every routed weight tensor the kernel would take,
     ahead of the first prefill chunk (engine/patches/moe-int8/patch.py:179-198).
-    Returns how many tensors were prepared."""
+    Returns how many tensors were prepared (0 with the tile cache off)."""
+    if not prepared.enabled():
+        return 0
     n = 0
     for m in switch_linears(model):
         if (m.bits, m.group_size, m.mode) != (_k.BITS, _k.GROUP, "affine") or m.bias is not None:

@@ -124,7 +124,13 @@ class SwitchGLU:
         self.gate_up_proj, self.gate_proj, self.up_proj = gate_up_proj, gate_proj, up_proj
         self.down_proj = down_proj
         # called as activation(x_up, x_gate), the reference's operand order
-        self.activation = SwiGLU() if activation is None else activation
+        # (that of the SwiGLU module).  The bare swiglu function takes
+        # (gate, x) instead (activations.py:9-11), so passed here it is
+        # wrapped in the module, which gives it the right halves; the
+        # reference would compute silu(up) * gate with it.
+        if activation is None or activation is swiglu:
+            activation = SwiGLU()
+        self.activation = activation
 
     @property
     def num_experts(self) -> int:
