@@ -58,6 +58,9 @@ def parse():
                     help="per-phase timestamps of the decode gate_up kernel (workload 1) from libqmoe_stamps.so")
     ap.add_argument("--traffic", action="store_true",
                     help="measure the decode kernel's HBM traffic live with rocprofv3 counter passes")
+    ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
+                    help="after timing each workload, replay its windows for SECONDS while sampling the "
+                         "board's socket power and gfx clocks (amd-smi)")
     return ap.parse_args()
 
 
@@ -366,6 +369,59 @@ def time_stamped(cycle, steps, warmup, dev, min_rounds=7):
 
 def timer(args):
     return time_eager if args.eager else time_stamped
+
+
+def sample_power(run_once, seconds):
+    """Socket power (W) and per-XCD gfx clocks (MHz) from `amd-smi metric -p -c`
+    sampled every ~0.25 s while `run_once` (one pass over a workload's windows)
+    repeats for `seconds`.  The first second of samples is dropped (the board
+    ramps to its limit).  Returns min / median / max of each, or the reason
+    there are none."""
+    import csv
+    import io
+    import shutil
+    import statistics
+    import subprocess
+    import threading
+
+    import torch
+
+    smi = shutil.which("amd-smi")
+    if smi is None:
+        return {"error": "amd-smi not found"}
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        t0 = time.perf_counter()
+        while not stop.is_set():
+            try:
+                out = subprocess.run([smi, "metric", "-p", "-c", "--csv"], capture_output=True, text=True,
+                                     timeout=10).stdout
+                rows = [ln for ln in out.splitlines() if ln.strip() and "," in ln]
+                row = next(csv.DictReader(io.StringIO("\n".join(rows))))
+                clk = [float(row[f"gfx_{i}_clk"]) for i in range(8) if row.get(f"gfx_{i}_clk", "N/A") != "N/A"]
+                samples.append((time.perf_counter() - t0, float(row["socket_power"]), statistics.mean(clk)))
+            except Exception:  # noqa: BLE001 - a missing field drops that sample
+                pass
+            stop.wait(0.25)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        run_once()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    kept = [s for s in samples if s[0] >= 1.0]
+    if not kept:
+        return {"error": "no samples", "raw": len(samples)}
+
+    def summ(v):
+        return {"min": round(min(v), 1), "median": round(statistics.median(v), 1), "max": round(max(v), 1)}
+
+    return {"socket_power_W": summ([s[1] for s in kept]), "gfx_clock_MHz": summ([s[2] for s in kept]),
+            "samples": len(kept), "seconds": seconds}
 
 
 # ------------------------------------------------------------ measured peaks
@@ -1017,7 +1073,7 @@ def decode_phases(args, dev, samples=16):
         "product_us_per_call": round(sec_prod * 1e6, 3),
         "samples": samples,
         "workload": meta["workload"],
-        "note": "stamps in 10 ns ticks, lane 0 of each of the flat kernel's 1024 single-wave blocks",
+        "note": "stamps in 10 ns ticks, lane 0 of each of the flat kernel's 1024 waves (four per workgroup)",
     }
     return res
 
@@ -1202,6 +1258,18 @@ def main():
             res[label] = {"us_per_call": round(sec_ex * 1e6, 3), "TOP/s": round(ex_flops / sec_ex / 1e12, 1),
                           "flops_per_call": ex_flops}
             del ex, _te
+        if args.power > 0:
+            graphs = tinfo.get("graphs")
+
+            def run_once(graphs=graphs, cycle=cycle):
+                if graphs:
+                    for g in graphs:
+                        g.replay()
+                else:
+                    for fn in cycle:
+                        fn()
+            res["power"] = sample_power(run_once, args.power)
+            print(f"[bench] workload {cfg} power: {res['power']}", file=sys.stderr, flush=True)
         results[cfg] = res
         print(f"[bench] workload {cfg}: {res}", file=sys.stderr, flush=True)
         if cfg == 1:
