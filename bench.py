@@ -448,11 +448,13 @@ def peaks_lib():
     return L
 
 
-def measure_peaks(dev, read_gib=4):
+def measure_peaks(dev, read_gib=4, power_seconds=0.0):
     """What this part sustains, with the probe kernels of libqmoe_peaks.so: a
     streaming read of `read_gib` GiB (beyond the 256 MB Infinity Cache) and
     dense bf16 / int8 MFMA loops over random register operands.  Medians of
-    five timed runs after one warm-up."""
+    five timed runs after one warm-up.  With power_seconds > 0 each probe is
+    then repeated for that long while the board's power and clocks are
+    sampled (sample_power)."""
     import statistics
 
     import torch
@@ -486,14 +488,28 @@ def measure_peaks(dev, read_gib=4):
     waves = L.qmoe_peak_mfma_waves()
     t_bf16 = timed(lambda: check(L.qmoe_peak_mfma_bf16(iters, sink.data_ptr(), st.cuda_stream)))
     t_i8 = timed(lambda: check(L.qmoe_peak_mfma_i8(iters, sink.data_ptr(), st.cuda_stream)))
+    power = None
+    if power_seconds > 0:
+        power = {
+            "stream_read": sample_power(
+                lambda: check(L.qmoe_peak_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), st.cuda_stream)),
+                power_seconds),
+            "mfma_bf16": sample_power(lambda: check(L.qmoe_peak_mfma_bf16(iters, sink.data_ptr(), st.cuda_stream)),
+                                      power_seconds),
+            "mfma_i8": sample_power(lambda: check(L.qmoe_peak_mfma_i8(iters, sink.data_ptr(), st.cuda_stream)),
+                                    power_seconds),
+        }
     del buf
     torch.cuda.empty_cache()
-    return {"hbm_read_GBps": round(nbytes / t_read / 1e9, 1),
+    res = {"hbm_read_GBps": round(nbytes / t_read / 1e9, 1),
             "bf16_mfma_TFLOPs": round(waves * iters * 4 * 32768 / t_bf16 / 1e12, 1),
             "int8_mfma_TOPs": round(waves * iters * 4 * 65536 / t_i8 / 1e12, 1),
             "method": f"stream read of {read_gib} GiB (16-byte non-temporal loads, 2048 blocks); "
                       f"{waves} waves x {iters} x 4 independent v_mfma_f32_32x32x16_bf16 / "
                       "v_mfma_i32_32x32x32_i8 on random register operands; median of 5"}
+    if power is not None:
+        res["power"] = power
+    return res
 
 
 # --------------------------------------------------------------- workloads
@@ -1193,7 +1209,7 @@ def main():
     peaks = None
     if args.only is None and not args.no_peaks:
         print("[bench] measured peaks", file=sys.stderr, flush=True)
-        peaks = measure_peaks(dev)
+        peaks = measure_peaks(dev, power_seconds=args.power)
         print(f"[bench] peaks: {peaks}", file=sys.stderr, flush=True)
     results = {}
     head = None
