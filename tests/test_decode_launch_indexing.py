@@ -14,6 +14,10 @@ the buffer it touches, at the workload shapes and at ragged edges:
   at workload 1's shape up to 12 KiB past x and 3 KiB past the last row).  That is the out-of-bounds access a 2- or 4-wave launch of the
   single-wave kernel makes.
 
+``qmv64_paired_lines_kernel`` (the tile-layout gate_up the one-copy MoE block
+decodes with) is modelled the same way: every access in bounds and every
+output index stored once, at the block's shapes and ragged ones.
+
 The reference's rule (a bounds test at the largest real shape before a kernel
 is enabled, docs/ops/INCIDENTS.md:29) is what this model gives on the CPU.
 """
@@ -183,3 +187,89 @@ def test_single_wave_indexing_overruns_in_wider_workgroups(W):
     # the same indexing at 64 threads (as the kernel was written) stays in bounds
     acc1, ext1 = flat_accesses(256, 10, 512, 1, 64, 1, 64, legacy=True)
     assert all(o <= 0 and lo >= 0 for lo, o in overruns(acc1, ext1).values())
+
+
+PAIRED_RG = int(re.search(r"#define QMOE_PAIRED_LINES_RG (\d+)", SRC.read_text()).group(1))
+
+
+def paired_lines_accesses(E, T, k, n_out, NV, W=1, RG=None):
+    """Byte ranges each buffer sees from one launch of qmv64_paired_lines_kernel
+    (tile-layout gate_up + SwiGLU, the form that takes expert ids): one 64-lane
+    wave per workgroup, item = xcd_item(block, grid), as launch_qmv_paired
+    sizes the grid.  (W > 1 models W waves per workgroup, item =
+    xcd_item(block) * W + wave, with per-wave LDS staging and waves past the
+    last item leaving.)"""
+    RG = RG or PAIRED_RG
+    NCH, NP, NJ = 64 * NV, 4 * NV, RG // 4
+    K = 2048 * NV
+    G = 32 * NV
+    n_w = 2 * n_out
+    NC = n_w // 64
+    n_pairs = T * k
+    nblk = n_out // RG
+    nitems = n_pairs * nblk
+    blocks = (nitems + W - 1) // W
+    threads = 64 * W
+    b = np.repeat(np.arange(blocks, dtype=np.int64), threads)
+    t = np.tile(np.arange(threads, dtype=np.int64), blocks)
+    lane, wave = t % 64, t // 64
+    item = xcd_item(b, blocks) * W + wave if W > 1 else xcd_item(b, blocks)
+    live = item < nitems
+    lane, wave, item = lane[live], wave[live], item[live]
+    r, sl = lane >> 3, lane & 7
+    jr = np.zeros_like(r) if RG == 8 else r >> 2
+    rr = r if RG == 8 else r & 3
+    pr = item // nblk
+    i0 = (item - pr * nblk) * RG
+    xr = pr // k
+    ids = (E - 1 - 7 * np.arange(n_pairs, dtype=np.int64)) % E
+    e = ids[pr]
+    c, l0 = i0 >> 5, i0 & 31
+    cbase = (e * NC + c) * G
+    acc = {"experts": [(pr * 4, pr * 4 + 4)], "x": [], "w": [], "sb": [], "lds": [], "out": []}
+    for v in range(NV):
+        lo = (xr * K + v * 2048 + lane * 32) * 2
+        acc["x"].append((lo, lo + 64))
+        for q in range(4):
+            lds = ((wave * 4 + q) * NCH + v * 64 + lane) * 16
+            acc["lds"].append((lds, lds + 16))
+    for pp in range(NP):
+        chunk = cbase + 8 * pp + sl
+        for jj in range(NJ):
+            wd = chunk * 64 + l0 + rr + 32 * (jr + jj)
+            acc["sb"].append((wd * 4, wd * 4 + 4))
+            for h in range(2):
+                u = ((chunk * 2 + jr + jj) * 2 + h) * 32 + l0 + rr
+                acc["w"].append((u * 16, u * 16 + 16))
+    m = (sl == 0) & (r < RG)
+    o = pr[m] * n_out + i0[m] + r[m]
+    acc["out"].append((o * 2, o * 2 + 2))
+    ext = {"experts": n_pairs * 4, "x": T * K * 2, "w": E * n_w * K // 2, "sb": E * NC * G * 64 * 4,
+           "lds": W * 4 * NCH * 16, "out": n_pairs * n_out * 2}
+    return acc, ext
+
+
+PAIRED_SHAPES = [
+    # E, tokens, top_k, I, NV: workload 1's block shape, two tokens, K = 4096,
+    # an item count that is not a multiple of W, and few experts
+    (256, 1, 10, 512, 1),
+    (256, 2, 10, 512, 1),
+    (256, 1, 8, 512, 2),
+    (64, 3, 7, 96, 1),
+    (4, 1, 3, 32, 1),
+]
+
+
+@pytest.mark.parametrize("E,T,k,n_out,NV", PAIRED_SHAPES)
+def test_paired_lines_kernel_accesses_in_bounds(E, T, k, n_out, NV):
+    acc, ext = paired_lines_accesses(E, T, k, n_out, NV)
+    for name, (lo, over) in overruns(acc, ext).items():
+        assert lo >= 0, (name, lo)
+        assert over <= 0, (name, over)
+
+
+@pytest.mark.parametrize("E,T,k,n_out,NV", PAIRED_SHAPES)
+def test_paired_lines_kernel_covers_every_output_once(E, T, k, n_out, NV):
+    acc, _ = paired_lines_accesses(E, T, k, n_out, NV)
+    stores = np.concatenate([r[0] for r in acc["out"]]) // 2
+    assert np.array_equal(np.sort(stores), np.arange(T * k * n_out))
