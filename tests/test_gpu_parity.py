@@ -728,6 +728,37 @@ def test_grouped_gemms_repeat_and_replay(dev, orc):
         torch.cuda.synchronize()
 
 
+def test_grouped_gemm_many_launches_in_a_row(dev, orc):
+    """150 launches of the bf16 grouped GEMM queued back to back (more than
+    the kernel's 64 unit-queue slots, so every slot is reused, and each launch
+    starts right after the previous one clears its slot) all give the first
+    launch's output bit for bit: no unit is skipped or taken twice."""
+    say("grouped GEMM: 150 launches in a row")
+    wl, r, lhs, order, srt, off = _prefill_routed(dev, orc, 1024)
+    t = r.tiles
+    xt = bf16_t(wl["x"], dev)
+    tw = ops.repack_tiles(words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev))
+    twp = ops.repack_tiles(words_t(wl["w"], dev), bf16_t(wl["s"], dev), bf16_t(wl["b"], dev), swiglu_pairs=True)
+    ref = ops.gather_qmm_sorted_tiles(xt, tw, t, x_rows=lhs)
+    ref_h = ops.gather_qmm_swiglu_sorted_tiles(xt, twp, t, x_rows=lhs)
+    torch.cuda.synchronize()
+    for batch in range(5):
+        outs = []
+        for i in range(30):
+            if i % 3 == 2:
+                outs.append(("swiglu", ops.gather_qmm_swiglu_sorted_tiles(xt, twp, t, x_rows=lhs)))
+            else:
+                outs.append(("bf16", ops.gather_qmm_sorted_tiles(xt, tw, t, x_rows=lhs)))
+        torch.cuda.synchronize()
+        for i, (kind, y) in enumerate(outs):
+            assert torch.equal(y, ref if kind == "bf16" else ref_h), (batch, i, kind)
+    rows = _sample_rows(off, int(wl["idx"].size), 128, np.random.default_rng(11))
+    k = wl["idx"].shape[1]
+    ref64, _ = orc.gather_qmm_rows(wl["x"], (order[rows] // k).astype(np.int32), srt[rows], wl["w"], wl["s"],
+                                   wl["b"], deq="bf16")
+    assert_close_bf16(orc, bits(ref)[rows], ref64, what="gemm tiles 1024 tokens, first launch")
+
+
 @pytest.mark.parametrize("tokens", [4096, 8192])
 def test_swiglu_gemm_tiles_prefill_sampled(dev, orc, tokens):
     """The SwiGLU-epilogue grouped GEMM (the block's prefill gate_up) at the
