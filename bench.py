@@ -54,6 +54,8 @@ def parse():
                     help="run one workload's timed loop only, or 'copy' for the calibration copy kernel")
     ap.add_argument("--eager", action="store_true", help="launch the timed steps eagerly (no graph)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak probes")
+    ap.add_argument("--gemm-units", action="store_true",
+                    help="per-unit timing of workload 3's grouped GEMM (measurement build) and exit")
     ap.add_argument("--decode-phases", action="store_true",
                     help="per-phase timestamps of the decode gate_up kernel (workload 1) from libqmoe_stamps.so")
     ap.add_argument("--traffic", action="store_true",
@@ -1094,6 +1096,92 @@ def decode_phases(args, dev, samples=16):
     return res
 
 
+def gemm_units(args, dev, samples=8):
+    """Workload 3's grouped GEMM through the measurement build
+    libqmoe_stamps.so, whose persistent blocks record s_memrealtime (10 ns
+    ticks) before and after each (tile, column block) unit.  Per subtile
+    count: units and median unit time, split by the block's half of the grid
+    (the first P/2 blocks are dispatched first, one per CU, so each CU holds
+    one of each); the blocks' end times and busy times; the kernel span."""
+    import ctypes
+
+    import torch
+    from titan_amd import _lib, build as tbuild, ops
+
+    base = _lib.load()
+    L = ctypes.CDLL(str(tbuild.STAMPS_LIB))
+    fn = L.qmoe_gather_qmm_sorted_tiles
+    fn.restype, fn.argtypes = ctypes.c_int, base.qmoe_gather_qmm_sorted_tiles.argtypes
+    rd = L.qmoe_gemm_stamps_read
+    rd.restype, rd.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    nu = int(L.qmoe_gemm_stamp_units())
+    wl, x, sets, r, lhs, out = _prefill_common(args, dev, 3)
+    t = r.tiles
+    tsets = [ops.repack_tiles(w, s_, b) for (w, s_, b) in sets]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    units_max = t.maxt * (1024 // 256)
+    P = min((2 * cus + 7) // 8 * 8, max(8, (units_max + 7) // 8 * 8))
+
+    def launch(i):
+        tw = tsets[i % len(tsets)]
+        rc = fn(x.data_ptr(), lhs.data_ptr(), t.rows, 2048, tw.wp.data_ptr(), tw.sb.data_ptr(), 256, 1024,
+                t.offsets.data_ptr(), t.tile_row.data_ptr(), t.tile_exp.data_ptr(), t.ntiles.data_ptr(), t.maxt,
+                out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"stamped qmoe_gather_qmm_sorted_tiles failed ({rc})")
+
+    for i in range(4):
+        launch(i)
+    torch.cuda.synchronize()
+    times = np.zeros(P * nu * 2, np.uint64)
+    uinfo = np.zeros(P * nu * 2, np.int32)
+    counts = np.zeros(P, np.int32)
+    recs, spans, ends_all, busy_all = [], [], [], []
+    for k in range(samples):
+        launch(k)
+        torch.cuda.synchronize()
+        if rd(times.ctypes.data, uinfo.ctypes.data, counts.ctypes.data, P) != 0:
+            raise RuntimeError("qmoe_gemm_stamps_read failed")
+        if counts.max() > nu:
+            raise RuntimeError(f"a block ran {counts.max()} units, more than the {nu} recorded")
+        tt = times.reshape(P, nu, 2).astype(np.int64)
+        ui = uinfo.reshape(P, nu, 2)
+        live = np.arange(nu)[None, :] < counts[:, None]
+        t0 = tt[..., 0][live].min()
+        blk = np.repeat(np.arange(P)[:, None], nu, axis=1)[live]
+        d = (tt[..., 1] - tt[..., 0])[live] * 0.01
+        msub = (ui[..., 1][live] + 31) // 32
+        recs.append((blk, d, msub))
+        end = np.where(live, tt[..., 1], 0).max(axis=1)
+        ran = counts > 0
+        ends_all.append((end[ran] - t0) * 0.01)
+        busy_all.append(np.where(live, tt[..., 1] - tt[..., 0], 0).sum(axis=1)[ran] * 0.01)
+        spans.append((end[ran].max() - t0) * 0.01)
+    blk = np.concatenate([r_[0] for r_ in recs])
+    d = np.concatenate([r_[1] for r_ in recs])
+    ms = np.concatenate([r_[2] for r_ in recs])
+    first = blk < P // 2
+    per = {}
+    for m in range(1, 5):
+        sel = ms == m
+        if sel.any():
+            per[str(m)] = {"units_per_launch": int(sel.sum() // samples),
+                           "median_us_first_half": round(float(np.median(d[sel & first])), 2) if (sel & first).any() else None,
+                           "median_us_second_half": round(float(np.median(d[sel & ~first])), 2) if (sel & ~first).any() else None}
+    pct = (0, 10, 50, 90, 100)
+    ends = np.concatenate(ends_all)
+    busy = np.concatenate(busy_all)
+    return {"workload": "workload 3 (prefill bf16 grouped GEMM, 4096 tokens)", "blocks": P, "samples": samples,
+            "unit_us_by_subtiles": per,
+            "percentiles": list(pct),
+            "block_end_us": [round(float(v), 1) for v in np.percentile(ends, pct)],
+            "block_busy_us": [round(float(v), 1) for v in np.percentile(busy, pct)],
+            "span_us_median": round(float(np.median(spans)), 1),
+            "busy_fraction_of_span": round(float(busy.mean() / np.median(spans)), 3),
+            "note": "eager launches of the stamped kernel; unit time from before the unit to after its "
+                    "epilogue stores are issued (lane 0 of the block); first half = blocks 0..P/2-1"}
+
+
 # ------------------------------------------------------------- CPU baseline
 
 
@@ -1205,6 +1293,9 @@ def main():
         cfgs = [int(args.only)]
     if args.decode_phases:
         print(json.dumps({"decode_phases": decode_phases(args, dev)}))
+        return 0
+    if args.gemm_units:
+        print(json.dumps({"gemm_units": gemm_units(args, dev)}))
         return 0
     peaks = None
     if args.only is None and not args.no_peaks:

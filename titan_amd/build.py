@@ -4,9 +4,10 @@ Each ``csrc/*.hip`` file is compiled to an object in parallel, then linked into
 ``titan_amd/lib/libqmoe.so``; ``csrc/peaks/peaks.hip`` (the bench's
 measured-ceiling probes, include/qmoe_peaks.h) becomes
 ``titan_amd/lib/libqmoe_peaks.so``; and ``titan_amd/lib/libqmoe_stamps.so`` is
-libqmoe.so with the decode GEMV's per-phase timestamps compiled in
-(QMOE_QMV_STAMPS, read by ``bench.py --decode-phases``), a measurement build
-that nothing else loads.  The libraries land in-tree so that they travel with
+libqmoe.so with the decode GEMV's per-phase timestamps and the bf16 grouped
+GEMM's per-unit timestamps compiled in (QMOE_QMV_STAMPS, QMOE_GEMM_STAMPS,
+read by ``bench.py --decode-phases`` and ``--gemm-units``), a measurement
+build that nothing else loads.  The libraries land in-tree so that they travel with
 the source tree; nothing is installed anywhere else.
 
     python -m titan_amd.build            # build (always recompiles)
@@ -79,12 +80,14 @@ def build(verbose: bool = False) -> Path:
     jobs = min(len(sources) + 1, max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
         fut_peaks = ex.submit(_compile, PEAKS_SRC)
-        fut_stamps = ex.submit(_compile, CSRC / "qmv.hip", "_stamps", ("QMOE_QMV_STAMPS",))
+        stamped = {"qmv": ex.submit(_compile, CSRC / "qmv.hip", "_stamps", ("QMOE_QMV_STAMPS",)),
+                   "gemm_bf16": ex.submit(_compile, CSRC / "gemm_bf16.hip", "_stamps", ("QMOE_GEMM_STAMPS",))}
         objs = list(ex.map(_compile, sources))
-        peaks_obj, stamps_obj = fut_peaks.result(), fut_stamps.result()
+        peaks_obj = fut_peaks.result()
+        stamped = {k: f.result() for k, f in stamped.items()}
     _link(objs, LIB)
     _link([peaks_obj], PEAKS_LIB)
-    _link([o if o.stem != "qmv" else stamps_obj for o in objs], STAMPS_LIB)
+    _link([stamped.get(o.stem, o) for o in objs], STAMPS_LIB)
     if verbose:
         print(f"built {LIB} from {len(sources)} sources, {PEAKS_LIB} and {STAMPS_LIB}")
     return LIB

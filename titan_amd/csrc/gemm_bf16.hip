@@ -55,6 +55,33 @@
 
 #include "gemm_common.h"
 
+#ifdef QMOE_GEMM_STAMPS
+// Measurement build only (libqmoe_stamps.so): lane 0 of each block records,
+// for each of its first kGemmStampUnits units, s_memrealtime (100 MHz) before
+// the unit and after the unit's epilogue stores are issued, the unit number
+// and its tile's row count; and after its loop, how many units it ran.  A
+// launch overwrites the records of its blocks.
+constexpr int kGemmStampBlocks = 1024;
+constexpr int kGemmStampUnits = 32;
+__device__ uint64_t gemm_stamps[kGemmStampBlocks * kGemmStampUnits * 2];
+__device__ int32_t gemm_stamp_units[kGemmStampBlocks * kGemmStampUnits * 2];
+__device__ int32_t gemm_stamp_counts[kGemmStampBlocks];
+
+extern "C" int qmoe_gemm_stamps_read(uint64_t* times, int32_t* units, int32_t* counts, int64_t nblocks) {
+  if (!times || !units || !counts || nblocks < 0 || nblocks > kGemmStampBlocks)
+    return qmoe::fail(QMOE_ERR_INVALID, "bad stamp request");
+  const size_t per = (size_t)nblocks * kGemmStampUnits * 2;
+  hipError_t e = hipMemcpyFromSymbol(times, HIP_SYMBOL(gemm_stamps), per * sizeof(uint64_t), 0, hipMemcpyDeviceToHost);
+  if (e == hipSuccess)
+    e = hipMemcpyFromSymbol(units, HIP_SYMBOL(gemm_stamp_units), per * sizeof(int32_t), 0, hipMemcpyDeviceToHost);
+  if (e == hipSuccess)
+    e = hipMemcpyFromSymbol(counts, HIP_SYMBOL(gemm_stamp_counts), (size_t)nblocks * sizeof(int32_t), 0,
+                            hipMemcpyDeviceToHost);
+  return e == hipSuccess ? QMOE_OK : qmoe::fail(QMOE_ERR_HIP, "hipMemcpyFromSymbol: %s", hipGetErrorString(e));
+}
+extern "C" int qmoe_gemm_stamp_units(void) { return kGemmStampUnits; }
+#endif
+
 namespace {
 
 using namespace qmoe_gemm;
@@ -555,13 +582,30 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void gemm_bf16_kernel(GemmA
   if (sn.unit(0) < 0) return;
   const bool sorted = ntiles <= kMaxOrder;
   if (sorted) rank_tiles(tt, ntiles, order, reinterpret_cast<int*>(smem));  // the ring is free until the first unit
-  for (int64_t k = 0;; ++k) {
+  int64_t k = 0;
+  for (;; ++k) {
     const int64_t u = sn.unit(k);
     if (u < 0) break;
     const int rank = (int)(u / NB);
     __syncthreads();  // every wave is done with the ring before it is refilled
+#ifdef QMOE_GEMM_STAMPS
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+#endif
     run_unit<TILED, SWIGLU>(a, smem, sorted ? order[rank] : rank, (int)(u % NB));
+#ifdef QMOE_GEMM_STAMPS
+    if (threadIdx.x == 0 && blockIdx.x < kGemmStampBlocks && k < kGemmStampUnits) {
+      const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+      const size_t o = ((size_t)blockIdx.x * kGemmStampUnits + k) * 2;
+      gemm_stamps[o] = t0;
+      gemm_stamps[o + 1] = t1;
+      gemm_stamp_units[o] = (int32_t)u;
+      gemm_stamp_units[o + 1] = tile_rows_of(tt, sorted ? order[rank] : rank).valid;
+    }
+#endif
   }
+#ifdef QMOE_GEMM_STAMPS
+  if (threadIdx.x == 0 && blockIdx.x < kGemmStampBlocks) gemm_stamp_counts[blockIdx.x] = (int32_t)k;
+#endif
 }
 
 }  // namespace
