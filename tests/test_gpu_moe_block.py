@@ -415,3 +415,43 @@ def test_moe_block_decode_top_k_past_tile_kernels(dev, orc, T):
     rep = orc.err_report(y, y64)
     print(f"[parity] block decode top_k={k} T={T}: {rep}", flush=True)
     assert rep["rel_to_max"] <= 2.0 ** -7
+
+
+@pytest.mark.parametrize("T,with_shared", [(1, False), (4, False), (1, True), (256, False), (256, True)])
+def test_moe_block_graph_replays(dev, T, with_shared):
+    """The whole block captured into a graph (the serving pattern: a static
+    input, new tokens copied in, the graph replayed) gives the eager result
+    bit for bit on every replay, with eager work between replays: decode
+    (the top-k gate_up and fused down kernels) and prefill (router top-k,
+    routing sort, the grouped GEMMs, the weighted sum), with and without the
+    shared expert."""
+    E, H, I, k = 64, 2048, 512, 8
+    say(f"MoE block graph replays T={T} shared={with_shared}")
+    gu, dn, router, sh = _block_problem(T + 31, E, H, I, with_shared=with_shared)
+    shared = None
+    if with_shared:
+        sgu, sdn, sg = sh
+        shared = moe_block.SharedExpert(_dev_w(sgu, dev), _dev_w(sdn, dev), bf16_t(sg, dev))
+    blk = moe_block.SparseMoeBlock(bf16_t(router, dev), _dev_w(gu, dev), _dev_w(dn, dev), k, shared=shared)
+    rng = np.random.default_rng(T + 77)
+    xs = [bf16_t(synth.bf16_bits(rng.normal(size=(T, H)).astype(np.float32)), dev) for _ in range(4)]
+    want = [blk(x).clone() for x in xs]
+    torch.cuda.synchronize()
+    static_x = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        blk(static_x)  # warm the allocator off the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_y = blk(static_x)
+    for rep in range(8):
+        i = (rep * 3) % len(xs)
+        static_x.copy_(xs[i])
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_y, want[i]), (T, with_shared, rep)
+        blk(xs[(i + 1) % len(xs)])  # eager work between replays
+        torch.cuda.synchronize()
