@@ -434,9 +434,10 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, char* smem, const 
 // paired row order): subtile j = 0 of a wave holds gate rows and j = 1 the
 // up rows of the same 32 intermediate indices, so every lane has both
 // operands of its h elements: h = silu(gate) * up in fp32 from the
-// accumulators (switch_layers.py:229-237, activations.py:9-11), rounded once
-// to bf16.  The block's 128 h columns leave through LDS as 256-byte row
-// segments, 16-byte unit u of staging row m at u ^ (m & 15).
+// accumulators (switch_layers.py:229-237, activations.py:9-11), with a
+// hardware reciprocal for the sigmoid's division, rounded once to bf16.  The
+// block's 128 h columns leave through LDS as 256-byte row segments, 16-byte
+// unit u of staging row m at u ^ (m & 15).
 template <bool TILED>
 __device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, char* smem, const Ctx<TILED>& c,
                                                   const f32x16_t (&acc)[kMaxSub][2], int64_t row0, int valid,
@@ -464,7 +465,10 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, char* smem,
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const float g = acc[i][0][4 * q + t], u = acc[i][1][4 * q + t];
-          hv[t] = g / (1.0f + __expf(-g)) * u;
+          // v_rcp_f32 (1 ulp in fp32, 2^-16 of a bf16 ulp) instead of an
+          // IEEE division: the division's ~10 VALU per output cost ~10 us
+          // of the 4096-token block
+          hv[t] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
         }
         const int gi = (c.wave * 32 + 8 * q + 4 * h) / 4;  // 8-byte granule within the 256-byte row
         const uint2 v = make_uint2(cvt_pk_bf16(hv[0], hv[1]), cvt_pk_bf16(hv[2], hv[3]));
