@@ -153,6 +153,16 @@ __device__ __forceinline__ float affine_chunk8(float dq, float xsum, float s, fl
   return s * (dq - 2176.0f * xsum) + b * xsum;
 }
 
+// SwiGLU of one output in fp32 (switch_layers.py:229-237,
+// activations.py:9-11): silu(gate) * up, the sigmoid through v_exp_f32 and
+// v_rcp_f32 (a few fp32 ulps, far below the bf16 rounding that follows)
+// rather than the library expf and an IEEE division, whose ~30 dependent
+// instructions sit at the end of every decode wave's chain.  Every decode
+// kernel uses this one expression, so their results stay bit-identical.
+__device__ __forceinline__ float swiglu_f32(float gate, float up) {
+  return gate * __builtin_amdgcn_rcpf(1.0f + __expf(-gate)) * up;
+}
+
 struct QmvArgs {
   const uint16_t* x;
   int64_t x_stride;      // elements between consecutive x rows
@@ -300,7 +310,7 @@ __global__ __launch_bounds__(64) void qmv_kernel(QmvArgs a) {
   if (MODE == 1) accu = group_sum<LPR>(accu);
   if (l == 0 && valid) {
     float o = accg;
-    if (MODE == 1) o = accg / (1.0f + expf(-accg)) * accu;
+    if (MODE == 1) o = swiglu_f32(accg, accu);
     if (MODE == 0 && a.out_f32) a.out_f32[r * a.n_out + n] = o;
     else a.out[r * a.n_out + n] = (uint16_t)f32_to_bf16(o);
   }
@@ -529,7 +539,7 @@ __device__ __forceinline__ void qmv64_rows(const QmvArgs& a) {
     auto sw = __builtin_amdgcn_permlane32_swap(as_u(t), as_u(t), false, false);
     const float up = as_f(sw[1]);
     if (lane < 32 && (lane & 7) == 0 && q < RG && n0 + q < a.n_out)
-      a.out[(int64_t)r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(t / (1.0f + expf(-t)) * up);
+      a.out[(int64_t)r * a.n_out + n0 + q] = (uint16_t)f32_to_bf16(swiglu_f32(t, up));
   } else {
     const int g = q >> 2, i = q & 3;
     const int n = (g == 0 ? n0 : grp1) + i;
@@ -755,7 +765,7 @@ __global__ __launch_bounds__(64 * W) void qmv64_flat_kernel(QmvArgs a) {
   const float gate = st4 ? t4 : t, up = as_f(st4 ? sw4[1] : sw[1]);
   const uint32_t f = f0 + (st4 ? 4u : (uint32_t)q);
   if (lane < 32 && ((lane & 7) == 0 || st4) && f < total)
-    aout[f] = (uint16_t)f32_to_bf16(gate / (1.0f + expf(-gate)) * up);
+    aout[f] = (uint16_t)f32_to_bf16(swiglu_f32(gate, up));
 #ifdef QMOE_QMV_STAMPS
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   QMV_STAMP(ts_stored);
@@ -935,7 +945,7 @@ __global__ __launch_bounds__(64) void qmv64_paired_kernel(QmvArgs a) {
     const float up = as_f(sw[1]);
     const int q = lane >> 3;
     if (lane < 32 && (lane & 7) == 0)
-      a.out[(int64_t)r * a.n_out + i0 + 4 * b + q] = (uint16_t)f32_to_bf16(t / (1.0f + expf(-t)) * up);
+      a.out[(int64_t)r * a.n_out + i0 + 4 * b + q] = (uint16_t)f32_to_bf16(swiglu_f32(t, up));
   }
 }
 
@@ -1061,7 +1071,7 @@ __global__ __launch_bounds__(64) void qmv64_paired_lines_kernel(QmvArgs a) {
     up = as_f(sw[1]);
   }
   if (sl == 0 && r < RG)
-    a.out[(int64_t)pr * a.n_out + i0 + r] = (uint16_t)f32_to_bf16(gate / (1.0f + expf(-gate)) * up);
+    a.out[(int64_t)pr * a.n_out + i0 + r] = (uint16_t)f32_to_bf16(swiglu_f32(gate, up));
 }
 
 struct DownArgs {
