@@ -54,15 +54,21 @@ def _route_cases():
     yield "uniform", rng.integers(0, 32, size=200).astype(np.int32), 32
     yield "single", np.array([3], np.int32), 8
     yield "ragged", rng.integers(0, 1000, size=12345).astype(np.int32), 1000
-    # the single-block path takes up to 8192 pairs and 512 experts
-    yield "fused-max", rng.integers(0, 512, size=8192).astype(np.int32), 512
-    yield "split-min", rng.integers(0, 512, size=8193).astype(np.int32), 512
+    # the single-block path takes up to 4096 pairs and 512 experts
+    yield "fused-max", rng.integers(0, 512, size=4096).astype(np.int32), 512
+    yield "split-min", rng.integers(0, 512, size=4097).astype(np.int32), 512
     yield "zipf-700", synth.make(3, tokens=700)["idx"], 256
-    # more than 2048 experts: the one-wave-per-chunk scatter
+    yield "zipf-300-fused", synth.make(3, tokens=300)["idx"], 256
+    yield "fused-ragged-waves", rng.integers(0, 40, size=1009).astype(np.int32), 40
+    # more than 2048 experts: the separate scan and the one-wave-per-chunk scatter
     yield "many-experts", rng.integers(0, 3000, size=9000).astype(np.int32), 3000
+    # more than 512 experts, up to 2048: the scatter that scans, whatever the size
+    yield "scan-scatter-max", rng.integers(0, 2048, size=20000).astype(np.int32), 2048
+    yield "one-chunk-many-experts", rng.integers(0, 1500, size=100).astype(np.int32), 1500
+    yield "empty-many-experts", np.zeros(0, np.int32), 1000
 
 
-@pytest.mark.parametrize("case", list(range(9)))
+@pytest.mark.parametrize("case", list(range(14)))
 def test_route_matches_stable_sort(dev, orc, case):
     name, ids, E = list(_route_cases())[case]
     say(f"route {name} n={ids.size} E={E}")
