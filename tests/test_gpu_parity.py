@@ -203,16 +203,19 @@ def test_weighted_sum_bit_exact(dev, orc, rows, dim, sorted_layout, mode):
     assert np.array_equal(bits(got).reshape(rows, dim), ref)
 
 
-@pytest.mark.parametrize("k", [6, 8])
-def test_weighted_sum_other_top_k(dev, orc, k):
-    say(f"weighted_sum k={k}")
+@pytest.mark.parametrize("k", [1, 6, 8, 16, 17, 20, 33])
+@pytest.mark.parametrize("mode", ["clone", "fast"])
+def test_weighted_sum_other_top_k(dev, orc, k, mode):
+    """Top-k below, at and past the kernel's batch of 16 slots (k = 33: three
+    batches, the last with one slot), and a row of 65 eight-column groups."""
+    say(f"weighted_sum k={k} mode={mode}")
     rng = np.random.default_rng(k)
-    rows, dim = 32, 512
+    rows, dim = 32, 520
     xs = synth.bf16_bits(rng.normal(size=(rows * k, dim)).astype(np.float32))
     sc = rng.uniform(size=(rows, k)).astype(np.float32)
     inv = rng.permutation(rows * k).astype(np.int32)
-    got = ops.moe_weighted_sum(bf16_t(xs, dev), i32_t(inv, dev), f32_t(sc, dev), (1, rows, dim))
-    assert np.array_equal(bits(got).reshape(rows, dim), orc.weighted_sum(xs, inv, sc, rows, k, dim, "clone"))
+    got = ops.moe_weighted_sum(bf16_t(xs, dev), i32_t(inv, dev), f32_t(sc, dev), (1, rows, dim), mode=mode)
+    assert np.array_equal(bits(got).reshape(rows, dim), orc.weighted_sum(xs, inv, sc, rows, k, dim, mode))
 
 
 # ------------------------------------------------------------- prefill GEMM

@@ -424,8 +424,11 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, char* smem, const 
     for (int it = 0; it < kIt; ++it) {
       const int m = it * (kThreads / 32) + tid / 32;
       const int row = kPassRows * p + m;
-      // block-uniform base + 32-bit offset: SGPR-based stores, no 64-bit row pointers
-      if (row < valid) *reinterpret_cast<i32x4_t*>(obase + (uint32_t)(row * a.N + (tid % 32) * 8)) = v[it];
+      // block-uniform base + 32-bit offset: SGPR-based stores, no 64-bit row
+      // pointers; non-temporal, as each output byte is written once and read,
+      // if at all, by a later launch (the 4096-token MoE block, whose down
+      // GEMM writes 168 MB, measured 411.0 -> 406.2 us with the hint)
+      if (row < valid) __builtin_nontemporal_store(v[it], reinterpret_cast<i32x4_t*>(obase + (uint32_t)(row * a.N + (tid % 32) * 8)));
     }
   }
 }
@@ -489,7 +492,7 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, char* smem,
     for (int it = 0; it < kIt; ++it) {
       const int m = it * (kThreads / 16) + tid / 16;
       const int row = kPassRows * p + m;
-      if (row < valid) *reinterpret_cast<i32x4_t*>(obase + (uint32_t)(row * NH + (tid % 16) * 8)) = v[it];
+      if (row < valid) __builtin_nontemporal_store(v[it], reinterpret_cast<i32x4_t*>(obase + (uint32_t)(row * NH + (tid % 16) * 8)));
     }
   }
 }

@@ -483,7 +483,10 @@ __device__ __forceinline__ void finish_tile(const Int8Args& a, char* smem, const
       const int u = tid % 32;
       const int row = 64 * p + m;
       const uint4 v = *reinterpret_cast<const uint4*>(ep + m * 512 + ((u ^ (2 * (m & 7))) * 16));
-      if (row < valid) *reinterpret_cast<uint4*>(obase + (int64_t)row * a.N + u * 8) = v;
+      if (row < valid) {  // non-temporal: written once, read (if at all) by a later launch
+        const i32x4_t t = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        __builtin_nontemporal_store(t, reinterpret_cast<i32x4_t*>(obase + (int64_t)row * a.N + u * 8));
+      }
     }
   }
 }

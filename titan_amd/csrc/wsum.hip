@@ -3,7 +3,10 @@
 // Each thread owns 8 adjacent columns of one output row and walks the k
 // expert outputs in order, keeping eight partial sums per column (slot j mod 8)
 // that are combined in slot order at the end.  Rows are fetched eight slots
-// at a time, so a thread has eight 16-byte loads in flight.  The arithmetic is spelled out
+// at a time, so a thread has eight 16-byte loads in flight.  Rows are read
+// and the output written with non-temporal hints: each byte is touched once
+// (measured 36.8 -> 32.4 us at 4096 tokens x top-10 x 2048 columns, 185 MB,
+// most of it from the store).  The arithmetic is spelled out
 // with contraction switched off so no multiply-add is fused: every mode is a
 // fixed sequence of IEEE operations and bf16 roundings, bit-for-bit
 // reproducible against a CPU restatement of the same sequence.
@@ -39,7 +42,8 @@ __global__ __launch_bounds__(256) void wsum_kernel(const uint16_t* __restrict__ 
         const int64_t p = r * k + j0 + jj;
         const int64_t src = inv ? (int64_t)inv[p] : p;
         sc[jj] = scores[p];
-        q[jj] = *reinterpret_cast<const uint4*>(xs + src * dim + c8);
+        const i32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(xs + src * dim + c8));
+        q[jj] = make_uint4((uint32_t)t[0], (uint32_t)t[1], (uint32_t)t[2], (uint32_t)t[3]);
       }
     }
 #pragma unroll
@@ -73,7 +77,8 @@ __global__ __launch_bounds__(256) void wsum_kernel(const uint16_t* __restrict__ 
     }
     o[v >> 1] = pack_bf16x2(r0, r1);
   }
-  *reinterpret_cast<uint4*>(out + r * dim + c8) = make_uint4(o[0], o[1], o[2], o[3]);
+  const i32x4_t ov = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+  __builtin_nontemporal_store(ov, reinterpret_cast<i32x4_t*>(out + r * dim + c8));
 }
 
 }  // namespace
