@@ -372,6 +372,22 @@ def test_quantize_act_int8_bit_exact(dev, orc):
     assert np.array_equal(xi.cpu().numpy(), rxi)
 
 
+@pytest.mark.parametrize("R,K", [(37, 512), (9, 1536), (5, 4096), (6, 5120), (3, 8192)])
+def test_quantize_act_int8_row_lengths(dev, orc, R, K):
+    """Rows of one to sixteen 512-element pieces per lane step, in registers
+    (K <= 4096) and read twice (K > 4096); an all-zero row and a row whose
+    maximum sits in its last element."""
+    say(f"int8 quantizer R={R} K={K}")
+    rng = np.random.default_rng(R * 31 + K)
+    x = synth.bf16_bits(rng.normal(size=(R, K)).astype(np.float32))
+    x[1] = 0
+    x[2, -1] = synth.bf16_bits(np.array([40.0], np.float32))[0]
+    xi, sx = ops.quantize_act_int8(bf16_t(x, dev))
+    rxi, rsx = orc.quant_act_int8(x)
+    assert np.array_equal(sx.cpu().numpy().view(np.uint32), rsx.view(np.uint32))
+    assert np.array_equal(xi.cpu().numpy(), rxi)
+
+
 @pytest.mark.parametrize("E,N,K,R", [(8, 256, 1024, 300), (16, 512, 2048, 640), (4, 768, 4096, 200),
                                      (8, 256, 1536, 90),
                                      (16, 2048, 512, 700)])  # the prefill down projection's shape (K = I = 512)

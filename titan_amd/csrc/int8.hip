@@ -19,9 +19,12 @@ namespace {
 
 // ---------------------------------------------------------------- quantizer
 
-// One wave per row; each lane owns K/64 consecutive elements (a multiple of 8).
-// Rows up to K = 4096 (64 elements per lane) stay in registers between the
-// max pass and the quantising pass; longer rows are read again.
+// One wave per row (K a multiple of 512); lane l owns the 8-element pieces
+// 64t + l, so each 16-byte load instruction of the wave reads 1 KiB of the
+// row contiguously (measured 10.4 -> 10.0 us at 4096 x 2048 and 21.7 -> 17.6
+// us at 4096 x 4096 against 64 consecutive elements per lane).  Rows up to
+// K = 4096 stay in registers between the max pass and the quantising pass;
+// longer rows are read again.
 constexpr int kQuantRegElems = 64;
 
 // 8 bf16 of one 16-byte load -> 8 int8, rint(x / sc) clamped to [-127, 127]
@@ -44,9 +47,9 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restri
   const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
   if (r >= R) return;
-  const int per = K / 64;
-  const uint16_t* xr = x + r * K + lane * per;
-  int8_t* out = xi + r * K + lane * per;
+  const int steps = K / 512;  // K % 512 == 0
+  const uint16_t* xr = x + r * K + lane * 8;
+  int8_t* out = xi + r * K + lane * 8;
   auto absmax8 = [](float m, const uint4 q) {
     const uint32_t v[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -55,27 +58,27 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restri
   };
   uint4 kept[kQuantRegElems / 8];
   float amax = 0.f;
-  if (per <= kQuantRegElems) {  // wave-uniform: static register indices, all loads in flight together
+  if (steps <= kQuantRegElems / 8) {  // wave-uniform: static register indices, all loads in flight together
 #pragma unroll
     for (int t = 0; t < kQuantRegElems / 8; ++t)
-      if (8 * t < per) kept[t] = *reinterpret_cast<const uint4*>(xr + 8 * t);
+      if (t < steps) kept[t] = *reinterpret_cast<const uint4*>(xr + 512 * t);
 #pragma unroll
     for (int t = 0; t < kQuantRegElems / 8; ++t)
-      if (8 * t < per) amax = absmax8(amax, kept[t]);
+      if (t < steps) amax = absmax8(amax, kept[t]);
   } else {
-    for (int i = 0; i < per; i += 8) amax = absmax8(amax, *reinterpret_cast<const uint4*>(xr + i));
+    for (int t = 0; t < steps; ++t) amax = absmax8(amax, *reinterpret_cast<const uint4*>(xr + 512 * t));
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
   const float sc = __fdiv_rn(amax, 127.0f);
   if (lane == 0) sx[r] = sc;
-  if (per <= kQuantRegElems) {
+  if (steps <= kQuantRegElems / 8) {
 #pragma unroll
     for (int t = 0; t < kQuantRegElems / 8; ++t)
-      if (8 * t < per) *reinterpret_cast<uint2*>(out + 8 * t) = quant_pack(kept[t], sc);
+      if (t < steps) *reinterpret_cast<uint2*>(out + 512 * t) = quant_pack(kept[t], sc);
   } else {
-    for (int i = 0; i < per; i += 8)
-      *reinterpret_cast<uint2*>(out + i) = quant_pack(*reinterpret_cast<const uint4*>(xr + i), sc);
+    for (int t = 0; t < steps; ++t)
+      *reinterpret_cast<uint2*>(out + 512 * t) = quant_pack(*reinterpret_cast<const uint4*>(xr + 512 * t), sc);
   }
 }
 
