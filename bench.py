@@ -1415,13 +1415,16 @@ def main():
     if fl is not None:
         # per-call floor of one launch that must learn its experts before
         # asking for their weights: the chain probe (launch, arguments, expert
-        # id, first row, store) plus the remaining bytes at the measured read rate
+        # id, first row, store) at the kernel's four waves per workgroup, plus
+        # the remaining bytes at the measured read rate
         floor = dict(fl)
         if peaks:
+            chain_us = fl.get("waves_per_block_4", {}).get("chain_us", fl["chain_us"])
             stream_us = (meta["bytes"] - fl["chain_bytes"]) / (peaks["hbm_read_GBps"] * 1e3)
             floor["stream_rest_us"] = round(stream_us, 3)
-            floor["model_us"] = round(fl["chain_us"] + stream_us, 3)
-            floor["frac_of_model"] = round((fl["chain_us"] + stream_us) / (sec * 1e6), 4)
+            floor["model_chain_us"] = chain_us
+            floor["model_us"] = round(chain_us + stream_us, 3)
+            floor["frac_of_model"] = round((chain_us + stream_us) / (sec * 1e6), 4)
         roof["floor"] = floor
     line = {
         "metric": METRIC,
