@@ -442,7 +442,8 @@ def peaks_lib():
             "qmoe_peak_mfma_i8": [c_int, c_vp, c_vp],
             "qmoe_peak_launch": [c_int, c_int, c_vp],
             "qmoe_peak_stamp": [c_vp, c_int, c_vp],
-            "qmoe_peak_chain": [c_vp, c_int, c_int, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp]}
+            "qmoe_peak_chain": [c_vp, c_int, c_int, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp],
+            "qmoe_peak_burst": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp]}
     for name, argtypes in sigs.items():
         fn = getattr(L, name)
         fn.restype = c_int
@@ -607,10 +608,22 @@ def setup_cfg1(args, dev):
             check(P.qmoe_peak_launch(1280, wpb, torch.cuda.current_stream().cuda_stream))
         return f
 
+    # the whole memory work after the ids: every wave reads all eight of its
+    # code rows and their scale and bias bytes (four-wave workgroups)
+    def mk_burst(i):
+        w, s_, b_ = sets[i % len(sets)]
+        idx = idxs[i]
+
+        def f():
+            check(P.qmoe_peak_burst(idx.data_ptr(), 10, E, w.data_ptr(), s_.data_ptr(), b_.data_ptr(), 1024, 64, 8, 4,
+                                    sink.data_ptr(), torch.cuda.current_stream().cuda_stream))
+        return f
+
     return wl, [mk_mlx(i) for i in range(L)], {
         # the same 1280 waves also in workgroups of two and four waves
         "floor": {"launch": [mk_launch(1)] * L, "chain": [mk_chain(i) for i in range(L)],
                   "wider": {w: ([mk_launch(w)] * L, [mk_chain(i, w) for i in range(L)]) for w in (2, 4)},
+                  "burst": [mk_burst(i) for i in range(L)], "burst_bytes": 10 * 1024 * (1024 + 2 * 64),
                   "chain_bytes": 1280 * 1024 + 10 * 4},
         "bytes": per_call, "flops": synth.algorithmic_flops(1), "bound": "hbm",
         "kernel": "qmv64_flat_kernel<1, 64, 4>", "sets": len(sets),
@@ -1359,6 +1372,11 @@ def main():
                 res["floor"][f"waves_per_block_{wpb}"] = {"launch_us": round(sl_ * 1e6, 3),
                                                           "chain_us": round(sc_ * 1e6, 3)}
                 del _x, _y
+            if "burst" in fl:
+                sb_, _z = timer(args)(fl["burst"], steps, args.warmup, dev)
+                res["floor"]["burst_us"] = round(sb_ * 1e6, 3)
+                res["floor"]["burst_bytes"] = fl["burst_bytes"]
+                del _z
             del fl, _tl, _tc
         for label, ex, ex_flops in meta.get("extras", ()):
             sec_ex, _te = timer(args)(ex, steps, args.warmup, dev)
@@ -1425,6 +1443,9 @@ def main():
             floor["model_chain_us"] = chain_us
             floor["model_us"] = round(chain_us + stream_us, 3)
             floor["frac_of_model"] = round((chain_us + stream_us) / (sec * 1e6), 4)
+        if "burst_us" in fl:
+            # the same ids-then-weights memory work measured as one launch
+            floor["frac_of_burst"] = round(fl["burst_us"] / (sec * 1e6), 4)
         roof["floor"] = floor
     line = {
         "metric": METRIC,

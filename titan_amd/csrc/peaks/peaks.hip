@@ -132,6 +132,37 @@ __global__ __launch_bounds__(64 * W) void chain_probe_kernel(const int32_t* __re
   if (lane == 0) sink[b] = acc;
 }
 
+// chain_probe_kernel's waves, each reading every one of its 8 rows of 1024
+// bytes (one 16-byte unit per lane and row, all eight in flight together)
+// and its rows' scale and bias units (lanes below sbu) after the id.
+template <int W>
+__global__ __launch_bounds__(64 * W) void burst_probe_kernel(const int32_t* __restrict__ ids, int blocks_per_slot,
+                                                             int num_experts, const i32x4_t* __restrict__ w,
+                                                             const i32x4_t* __restrict__ s,
+                                                             const i32x4_t* __restrict__ b, int64_t expert_units,
+                                                             int64_t sexpert_units, int sbu,
+                                                             uint32_t* __restrict__ sink) {
+  constexpr int kRows = 8;
+  const int lane = threadIdx.x % 64;
+  const uint32_t item = blockIdx.x * W + threadIdx.x / 64;
+  const uint32_t slot = item / (uint32_t)blocks_per_slot;
+  const uint32_t rb = item - slot * (uint32_t)blocks_per_slot;
+  int e = ids[slot];
+  e = min(max(e, 0), num_experts - 1);
+  const i32x4_t* wp = w + (int64_t)e * expert_units + (int64_t)rb * (kRows * 64) + lane;
+  i32x4_t v[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) v[r] = __builtin_nontemporal_load(wp + r * 64);
+  const int su = min(lane, sbu - 1);
+  const int64_t so = (int64_t)e * sexpert_units + (int64_t)rb * sbu + su;
+  const i32x4_t sv = __builtin_nontemporal_load(s + so), bv = __builtin_nontemporal_load(b + so);
+  uint32_t acc = lane < sbu ? (uint32_t)(sv[0] ^ sv[1] ^ bv[2] ^ bv[3]) : 0u;
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) acc ^= (uint32_t)(v[r][0] ^ v[r][1] ^ v[r][2] ^ v[r][3]);
+  for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m, 64);
+  if (lane == 0) sink[item] = acc;
+}
+
 // One wave writes the GPU's constant 100 MHz clock (s_memrealtime) to
 // stamps[slot] with a vector store: placed between the timed windows of one
 // graph, it times each window from the GPU without a graph launch inside it.
@@ -196,6 +227,39 @@ extern "C" int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, c
   if (waves_per_block == 1) chain_probe_kernel<1><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
   else if (waves_per_block == 2) chain_probe_kernel<2><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
   else chain_probe_kernel<4><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, eu, bu, sink);
+  return status();
+}
+
+extern "C" int qmoe_peak_burst(const int32_t* ids, int slots, int num_experts, const void* w, const void* s,
+                               const void* b, int rows_per_expert, int srow_bytes, int rows_per_block,
+                               int waves_per_block, uint32_t* sink, void* stream) {
+  // wave (slot, rb) reads units [rb * 512, rb * 512 + 512) of its expert's
+  // rows_per_expert * 64 code units and units [rb * sbu, rb * sbu + sbu) of
+  // its expert's scale and bias units: in bounds when the row blocks tile
+  // the rows; the work items are 0 .. slots * blocks_per_slot - 1 exactly
+  if (!ids || !w || !s || !b || !sink || slots <= 0 || num_experts <= 0 || rows_per_expert <= 0 ||
+      rows_per_block != 8 || rows_per_expert % rows_per_block || srow_bytes <= 0 ||
+      (rows_per_block * srow_bytes) % 16 || rows_per_block * srow_bytes > 1024 ||
+      ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(s) | reinterpret_cast<uintptr_t>(b)) & 15) ||
+      (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4))
+    return 1;
+  const int blocks_per_slot = rows_per_expert / rows_per_block;
+  const int64_t items = (int64_t)slots * blocks_per_slot;
+  if (items % waves_per_block || items > 0x7FFFFFFF) return 1;
+  const int sbu = rows_per_block * srow_bytes / 16;
+  const int64_t eu = (int64_t)rows_per_expert * 64, seu = (int64_t)rows_per_expert * srow_bytes / 16;
+  if ((int64_t)rows_per_expert * srow_bytes % 16) return 1;
+  const dim3 grid((uint32_t)(items / waves_per_block)), block(64 * waves_per_block);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const i32x4_t* wp = static_cast<const i32x4_t*>(w);
+  const i32x4_t* sp = static_cast<const i32x4_t*>(s);
+  const i32x4_t* bp = static_cast<const i32x4_t*>(b);
+  if (waves_per_block == 1)
+    burst_probe_kernel<1><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
+  else if (waves_per_block == 2)
+    burst_probe_kernel<2><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
+  else
+    burst_probe_kernel<4><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
   return status();
 }
 
