@@ -443,7 +443,7 @@ def peaks_lib():
             "qmoe_peak_launch": [c_int, c_int, c_vp],
             "qmoe_peak_stamp": [c_vp, c_int, c_vp],
             "qmoe_peak_chain": [c_vp, c_int, c_int, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp],
-            "qmoe_peak_burst": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp]}
+            "qmoe_peak_burst": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp]}
     for name, argtypes in sigs.items():
         fn = getattr(L, name)
         fn.restype = c_int
@@ -615,8 +615,8 @@ def setup_cfg1(args, dev):
         idx = idxs[i]
 
         def f():
-            check(P.qmoe_peak_burst(idx.data_ptr(), 10, E, w.data_ptr(), s_.data_ptr(), b_.data_ptr(), 1024, 64, 8, 4,
-                                    sink.data_ptr(), torch.cuda.current_stream().cuda_stream))
+            check(P.qmoe_peak_burst(idx.data_ptr(), 10, E, w.data_ptr(), s_.data_ptr(), b_.data_ptr(), 1024, 1024, 64,
+                                    8, 4, sink.data_ptr(), torch.cuda.current_stream().cuda_stream))
         return f
 
     return wl, [mk_mlx(i) for i in range(L)], {
@@ -713,6 +713,23 @@ def setup_cfg2(args, dev):
                           torch.cuda.current_stream().cuda_stream)
         return f
 
+    # the floor of this launch shape (libqmoe_peaks.so): 10,240 waves in
+    # ten-wave workgroups, each reading its pair's expert id, then its 16 rows
+    # of codes (4 KiB) and their scales and biases, with no arithmetic
+    P = peaks_lib()
+    sink = torch.zeros(10240, dtype=torch.int32, device=dev)
+
+    def mk_burst(i):
+        w, s_, b_ = sets[i % len(sets)]
+        ii = idxs[i]
+
+        def f():
+            rc = P.qmoe_peak_burst(ii.data_ptr(), 80, 256, w.data_ptr(), s_.data_ptr(), b_.data_ptr(), 2048, 256, 16,
+                                   16, 10, sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"floor probe failed (code {rc})")
+        return f
+
     mean_distinct = float(np.mean(distinct))
     row_bytes = 512 // 2 + 8 * 4
     bytes_ = int(mean_distinct * 2048 * row_bytes + 8 * 10 * 512 * 2 + 8 * 2048 * 2 + 8 * 10 * 4)
@@ -720,6 +737,7 @@ def setup_cfg2(args, dev):
         "bytes": bytes_, "flops": synth.algorithmic_flops(2, wl), "bound": "hbm",
         "kernel": "down_pair_kernel<16>", "sets": len(sets), "mean_distinct_experts": mean_distinct,
         "cycle_bytes": L * bytes_, "alt": ("tile_layout_us_per_call", [mk_tiles(i) for i in range(L)]),
+        "floor": {"burst": [mk_burst(i) for i in range(L)], "burst_bytes": 80 * 2048 * (256 + 2 * 16)},
         "workload": "decode down + top-10 weighted sum: 8 tokens, I=512, D=2048, E=256, "
                     "W [256,2048,512] int4 g64 -> y [8,2048]"}
 
@@ -1362,10 +1380,13 @@ def main():
             del alt, _ta
         if "floor" in meta:
             fl = meta.pop("floor")
-            sec_l, _tl = timer(args)(fl["launch"], steps, args.warmup, dev)
-            sec_c, _tc = timer(args)(fl["chain"], steps, args.warmup, dev)
-            res["floor"] = {"launch_us": round(sec_l * 1e6, 3), "chain_us": round(sec_c * 1e6, 3),
-                            "chain_bytes": fl["chain_bytes"]}
+            res["floor"] = {}
+            if "launch" in fl:
+                sec_l, _tl = timer(args)(fl["launch"], steps, args.warmup, dev)
+                sec_c, _tc = timer(args)(fl["chain"], steps, args.warmup, dev)
+                res["floor"].update(launch_us=round(sec_l * 1e6, 3), chain_us=round(sec_c * 1e6, 3),
+                                    chain_bytes=fl["chain_bytes"])
+                del _tl, _tc
             for wpb, (wl_, wc_) in fl.get("wider", {}).items():
                 sl_, _x = timer(args)(wl_, steps, args.warmup, dev)
                 sc_, _y = timer(args)(wc_, steps, args.warmup, dev)
@@ -1376,8 +1397,9 @@ def main():
                 sb_, _z = timer(args)(fl["burst"], steps, args.warmup, dev)
                 res["floor"]["burst_us"] = round(sb_ * 1e6, 3)
                 res["floor"]["burst_bytes"] = fl["burst_bytes"]
+                res["floor"]["frac_of_burst"] = round(sb_ / sec, 4)
                 del _z
-            del fl, _tl, _tc
+            del fl
         for label, ex, ex_flops in meta.get("extras", ()):
             sec_ex, _te = timer(args)(ex, steps, args.warmup, dev)
             res[label] = {"us_per_call": round(sec_ex * 1e6, 3), "TOP/s": round(ex_flops / sec_ex / 1e12, 1),

@@ -46,16 +46,17 @@ int qmoe_peak_launch(int waves, int waves_per_block, void* stream);
 int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, const void* w, int rows_per_expert,
                     int row_bytes, int rows_per_block, int waves_per_block, uint32_t* sink, void* stream);
 
-/* qmoe_peak_burst: qmoe_peak_chain's waves, each reading all of its
- * rows_per_block rows of 1024 bytes after the id (rows_per_block = 8: eight
- * 16-byte loads per lane) and the rows' scale and bias bytes, srow_bytes per
- * row in s and in b (num_experts x rows_per_expert rows each, 16-byte aligned;
- * rows_per_block * srow_bytes a multiple of 16 and at most 1024): the memory
- * work of a decode GEMV that learns its experts before reading their weights,
- * without its arithmetic.  Returns 1 on arguments that break these rules. */
+/* qmoe_peak_burst: qmoe_peak_chain's waves, each reading, after its id, all
+ * of its rows_per_block rows of row_bytes bytes (contiguous: 4 or 8 KiB per
+ * wave, one 16-byte load per lane and KiB) and the rows' scale and bias
+ * bytes, srow_bytes per row in s and in b (num_experts x rows_per_expert rows
+ * each, 16-byte aligned; rows_per_block * srow_bytes a multiple of 16 and at
+ * most 1024), in workgroups of 1, 2, 4 or 10 waves: the memory work of a
+ * decode GEMV that learns its experts before reading their weights, without
+ * its arithmetic.  Returns 1 on arguments that break these rules. */
 int qmoe_peak_burst(const int32_t* ids, int slots, int num_experts, const void* w, const void* s, const void* b,
-                    int rows_per_expert, int srow_bytes, int rows_per_block, int waves_per_block, uint32_t* sink,
-                    void* stream);
+                    int rows_per_expert, int row_bytes, int srow_bytes, int rows_per_block, int waves_per_block,
+                    uint32_t* sink, void* stream);
 
 /* One single-wave launch that writes the GPU's constant 100 MHz clock
  * (s_memrealtime, 10 ns ticks) to stamps[slot] (slot >= 0, within the

@@ -132,33 +132,32 @@ __global__ __launch_bounds__(64 * W) void chain_probe_kernel(const int32_t* __re
   if (lane == 0) sink[b] = acc;
 }
 
-// chain_probe_kernel's waves, each reading every one of its 8 rows of 1024
-// bytes (one 16-byte unit per lane and row, all eight in flight together)
+// chain_probe_kernel's waves, each reading all of its contiguous rows,
+// LOADS KiB (one 16-byte unit per lane and KiB, all in flight together),
 // and its rows' scale and bias units (lanes below sbu) after the id.
-template <int W>
+template <int W, int LOADS>
 __global__ __launch_bounds__(64 * W) void burst_probe_kernel(const int32_t* __restrict__ ids, int blocks_per_slot,
                                                              int num_experts, const i32x4_t* __restrict__ w,
                                                              const i32x4_t* __restrict__ s,
                                                              const i32x4_t* __restrict__ b, int64_t expert_units,
                                                              int64_t sexpert_units, int sbu,
                                                              uint32_t* __restrict__ sink) {
-  constexpr int kRows = 8;
   const int lane = threadIdx.x % 64;
   const uint32_t item = blockIdx.x * W + threadIdx.x / 64;
   const uint32_t slot = item / (uint32_t)blocks_per_slot;
   const uint32_t rb = item - slot * (uint32_t)blocks_per_slot;
   int e = ids[slot];
   e = min(max(e, 0), num_experts - 1);
-  const i32x4_t* wp = w + (int64_t)e * expert_units + (int64_t)rb * (kRows * 64) + lane;
-  i32x4_t v[kRows];
+  const i32x4_t* wp = w + (int64_t)e * expert_units + (int64_t)rb * (LOADS * 64) + lane;
+  i32x4_t v[LOADS];
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) v[r] = __builtin_nontemporal_load(wp + r * 64);
+  for (int r = 0; r < LOADS; ++r) v[r] = __builtin_nontemporal_load(wp + r * 64);
   const int su = min(lane, sbu - 1);
   const int64_t so = (int64_t)e * sexpert_units + (int64_t)rb * sbu + su;
   const i32x4_t sv = __builtin_nontemporal_load(s + so), bv = __builtin_nontemporal_load(b + so);
   uint32_t acc = lane < sbu ? (uint32_t)(sv[0] ^ sv[1] ^ bv[2] ^ bv[3]) : 0u;
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) acc ^= (uint32_t)(v[r][0] ^ v[r][1] ^ v[r][2] ^ v[r][3]);
+  for (int r = 0; r < LOADS; ++r) acc ^= (uint32_t)(v[r][0] ^ v[r][1] ^ v[r][2] ^ v[r][3]);
   for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m, 64);
   if (lane == 0) sink[item] = acc;
 }
@@ -230,37 +229,50 @@ extern "C" int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, c
   return status();
 }
 
+template <int LOADS>
+int launch_burst(dim3 grid, int waves_per_block, hipStream_t st, const int32_t* ids, int blocks_per_slot,
+                 int num_experts, const i32x4_t* wp, const i32x4_t* sp, const i32x4_t* bp, int64_t eu, int64_t seu,
+                 int sbu, uint32_t* sink) {
+  const dim3 block(64 * waves_per_block);
+  switch (waves_per_block) {
+    case 1: burst_probe_kernel<1, LOADS><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink); break;
+    case 2: burst_probe_kernel<2, LOADS><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink); break;
+    case 4: burst_probe_kernel<4, LOADS><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink); break;
+    default: burst_probe_kernel<10, LOADS><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink); break;
+  }
+  return status();
+}
+
 extern "C" int qmoe_peak_burst(const int32_t* ids, int slots, int num_experts, const void* w, const void* s,
-                               const void* b, int rows_per_expert, int srow_bytes, int rows_per_block,
+                               const void* b, int rows_per_expert, int row_bytes, int srow_bytes, int rows_per_block,
                                int waves_per_block, uint32_t* sink, void* stream) {
-  // wave (slot, rb) reads units [rb * 512, rb * 512 + 512) of its expert's
-  // rows_per_expert * 64 code units and units [rb * sbu, rb * sbu + sbu) of
-  // its expert's scale and bias units: in bounds when the row blocks tile
-  // the rows; the work items are 0 .. slots * blocks_per_slot - 1 exactly
+  // wave (slot, rb) reads code units [rb * 64 L, rb * 64 L + 64 L) of its
+  // expert's rows_per_expert * row_bytes / 16 (L = rows_per_block * row_bytes
+  // / 1024 = 4 or 8) and units [rb * sbu, rb * sbu + sbu) of its expert's
+  // scale and bias units: in bounds when the row blocks tile the rows; the
+  // work items are 0 .. slots * blocks_per_slot - 1 exactly
   if (!ids || !w || !s || !b || !sink || slots <= 0 || num_experts <= 0 || rows_per_expert <= 0 ||
-      rows_per_block != 8 || rows_per_expert % rows_per_block || srow_bytes <= 0 ||
-      (rows_per_block * srow_bytes) % 16 || rows_per_block * srow_bytes > 1024 ||
+      rows_per_block <= 0 || row_bytes <= 0 || row_bytes % 16 || rows_per_expert % rows_per_block ||
+      srow_bytes <= 0 || (rows_per_block * srow_bytes) % 16 || rows_per_block * srow_bytes > 1024 ||
+      ((int64_t)rows_per_expert * srow_bytes) % 16 ||
       ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(s) | reinterpret_cast<uintptr_t>(b)) & 15) ||
-      (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4))
+      (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4 && waves_per_block != 10))
     return 1;
+  const int64_t block_bytes = (int64_t)rows_per_block * row_bytes;
+  if (block_bytes != 4096 && block_bytes != 8192) return 1;
   const int blocks_per_slot = rows_per_expert / rows_per_block;
   const int64_t items = (int64_t)slots * blocks_per_slot;
   if (items % waves_per_block || items > 0x7FFFFFFF) return 1;
   const int sbu = rows_per_block * srow_bytes / 16;
-  const int64_t eu = (int64_t)rows_per_expert * 64, seu = (int64_t)rows_per_expert * srow_bytes / 16;
-  if ((int64_t)rows_per_expert * srow_bytes % 16) return 1;
-  const dim3 grid((uint32_t)(items / waves_per_block)), block(64 * waves_per_block);
+  const int64_t eu = (int64_t)rows_per_expert * row_bytes / 16, seu = (int64_t)rows_per_expert * srow_bytes / 16;
+  const dim3 grid((uint32_t)(items / waves_per_block));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const i32x4_t* wp = static_cast<const i32x4_t*>(w);
   const i32x4_t* sp = static_cast<const i32x4_t*>(s);
   const i32x4_t* bp = static_cast<const i32x4_t*>(b);
-  if (waves_per_block == 1)
-    burst_probe_kernel<1><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
-  else if (waves_per_block == 2)
-    burst_probe_kernel<2><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
-  else
-    burst_probe_kernel<4><<<grid, block, 0, st>>>(ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
-  return status();
+  if (block_bytes == 4096)
+    return launch_burst<4>(grid, waves_per_block, st, ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
+  return launch_burst<8>(grid, waves_per_block, st, ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
 }
 
 extern "C" int qmoe_peak_stamp(uint64_t* stamps, int slot, void* stream) {
