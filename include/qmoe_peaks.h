@@ -47,7 +47,7 @@ int qmoe_peak_chain(const int32_t* ids, int slots, int num_experts, const void* 
                     int row_bytes, int rows_per_block, int waves_per_block, uint32_t* sink, void* stream);
 
 /* qmoe_peak_burst: qmoe_peak_chain's waves, each reading, after its id, all
- * of its rows_per_block rows of row_bytes bytes (contiguous: 4 or 8 KiB per
+ * of its rows_per_block rows of row_bytes bytes (contiguous: 4, 8 or 16 KiB per
  * wave, one 16-byte load per lane and KiB) and the rows' scale and bias
  * bytes, srow_bytes per row in s and in b (num_experts x rows_per_expert rows
  * each, 16-byte aligned; rows_per_block * srow_bytes a multiple of 16 and at

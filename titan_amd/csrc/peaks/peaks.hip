@@ -248,7 +248,7 @@ extern "C" int qmoe_peak_burst(const int32_t* ids, int slots, int num_experts, c
                                int waves_per_block, uint32_t* sink, void* stream) {
   // wave (slot, rb) reads code units [rb * 64 L, rb * 64 L + 64 L) of its
   // expert's rows_per_expert * row_bytes / 16 (L = rows_per_block * row_bytes
-  // / 1024 = 4 or 8) and units [rb * sbu, rb * sbu + sbu) of its expert's
+  // / 1024 = 4, 8 or 16) and units [rb * sbu, rb * sbu + sbu) of its expert's
   // scale and bias units: in bounds when the row blocks tile the rows; the
   // work items are 0 .. slots * blocks_per_slot - 1 exactly
   if (!ids || !w || !s || !b || !sink || slots <= 0 || num_experts <= 0 || rows_per_expert <= 0 ||
@@ -259,7 +259,7 @@ extern "C" int qmoe_peak_burst(const int32_t* ids, int slots, int num_experts, c
       (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4 && waves_per_block != 10))
     return 1;
   const int64_t block_bytes = (int64_t)rows_per_block * row_bytes;
-  if (block_bytes != 4096 && block_bytes != 8192) return 1;
+  if (block_bytes != 4096 && block_bytes != 8192 && block_bytes != 16384) return 1;
   const int blocks_per_slot = rows_per_expert / rows_per_block;
   const int64_t items = (int64_t)slots * blocks_per_slot;
   if (items % waves_per_block || items > 0x7FFFFFFF) return 1;
@@ -272,7 +272,9 @@ extern "C" int qmoe_peak_burst(const int32_t* ids, int slots, int num_experts, c
   const i32x4_t* bp = static_cast<const i32x4_t*>(b);
   if (block_bytes == 4096)
     return launch_burst<4>(grid, waves_per_block, st, ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
-  return launch_burst<8>(grid, waves_per_block, st, ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
+  if (block_bytes == 8192)
+    return launch_burst<8>(grid, waves_per_block, st, ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
+  return launch_burst<16>(grid, waves_per_block, st, ids, blocks_per_slot, num_experts, wp, sp, bp, eu, seu, sbu, sink);
 }
 
 extern "C" int qmoe_peak_stamp(uint64_t* stamps, int slot, void* stream) {
